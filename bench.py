@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""bench.py -- paged decode attention at the Llama-3-8B shape on one MI355X.
+
+Workload (the metric's config): 32 query heads,
+8 KV heads, head_dim 128, bf16 Q/K/V ~ N(0, 1); 64 sequences with context
+lengths uniform in [512, 4096] (seed 2); block size 16; block tables are
+disjoint slices of a seeded permutation of a 20000-block pool.
+
+One step = what the engine does per layer for this batch
+(crates/engine/src/model.rs:309-319): write_kv of the 64 new tokens
+(reshape_and_cache), then decode_attention over ctx + 1 keys per sequence
+(split-K kernel + reduce kernel).  Steps alternate between two pool layers
+(2.6 GB) so that the 256 MB MALL cannot serve one step's KV from the last.
+
+value = algorithmic decode bytes per step / step time, in GB/s, where the
+algorithmic bytes are every key's K and V once per KV head (bf16), the q and
+out rows, and the block-table entries.  tokens_per_s = 64 / step time.
+roofline.achieved = the same bytes / the split-K kernel's average duration,
+timed live with HIP events around each launch.
+
+--config cfg3 / cfg5 print an extra line for the prefill and prefix-shared
+decode configs.
+"""
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
+
+METRIC = "paged decode attn HBM GB/s (% of peak) + tokens/s, Llama-3-8B shape, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def _load_package():
+    import __graft_entry__ as g
+    return g._load_package()
+
+
+def cpu_info():
+    model = platform.processor() or ""
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, avail
+
+
+def traffic_record(kernel, workload):
+    """Counter-measured HBM bytes per launch, from the committed rocprofv3
+    --pmc summary for this kernel and workload (profiles/*.json), or None."""
+    for p in sorted((ROOT / "profiles").glob("*.json")):
+        try:
+            rec = json.loads(p.read_text())
+        except (OSError, ValueError):
+            continue
+        if rec.get("kernel") == kernel and rec.get("workload") == workload:
+            return rec.get("hbm_bytes_per_launch")
+    return None
+
+
+def time_steps(torch, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def bench_decode(vo, W, orc, args, cfg):
+    import torch
+    heads, kvh, hd, bs = cfg["heads"], 8, 128, 16
+    ctx = cfg["ctx"]
+    layers = args.layers
+    backend = vo.HipBackend(device=0, max_seqs=len(ctx), max_rows=W.FILL_ROWS,
+                            max_table_entries=cfg["num_blocks"], max_query_heads=heads)
+    wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=bs, num_blocks=cfg["num_blocks"], context_lens=ctx, seed=cfg["seed"],
+                 num_layers=layers, fill_layers=list(range(layers)),
+                 shared_prefix=cfg.get("shared_prefix", 0),
+                 shared_count=cfg.get("shared_count", 0), keep_host=not args.no_cpu)
+    S = len(ctx)
+    out = torch.empty_like(wl.q)
+    # The step's metadata crosses to the device once (as in a real step, where
+    # all layers share it); the ops below then take raw C-ABI arguments.
+    backend.write_kv(wl.pool, 0, wl.k_new, wl.v_new, wl.meta)
+    meta_h = backend.step_meta(wl.pool).handle
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lib = vo.lib
+    kp, vp = ctypes.c_void_p(wl.k_new.data_ptr()), ctypes.c_void_p(wl.v_new.data_ptr())
+    qp, op = ctypes.c_void_p(wl.q.data_ptr()), ctypes.c_void_p(out.data_ptr())
+    width = kvh * hd
+
+    def step(i):
+        layer = i % layers
+        rc = lib.vo_write_kv(wl.pool.handle, layer, kp, vp, S, width, meta_h, stream)
+        rc |= lib.vo_decode_attention(qp, S, heads * hd, wl.pool.handle, layer, meta_h, op, stream)
+        if rc:
+            raise RuntimeError(f"C-ABI call failed: {rc}")
+
+    sec = time_steps(torch, step, args.steps, args.warmup)
+    # Per-kernel durations, live, over a second timed pass with event timing on.
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    sec_prof = time_steps(torch, step, args.steps, 0)
+    vo.enable_profiling(False)
+    prof = vo.profile()
+
+    nbytes = wl.decode_bytes()
+    gbs = nbytes / sec / 1e9
+    split = prof.get("decode_splitk", {})
+    split_s = split.get("avg_ms", 0.0) / 1e3
+    achieved = nbytes / split_s / 1e9 if split_s else None
+    workload_name = cfg["name"]
+    traffic = traffic_record("decode_splitk", workload_name)
+    line = {
+        "metric": METRIC if cfg["name"].startswith("cfg2") else cfg["metric"],
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": workload_name,
+            "seqs": S, "query_heads": heads, "kv_heads": kvh, "head_dim": hd, "block_size": bs,
+            "pool_blocks": cfg["num_blocks"], "context": cfg["ctx_desc"],
+            "keys_total": int(wl.row_num_keys().sum()),
+            "step": "write_kv(new tokens) + decode_attention (split-K + reduce)",
+            "layers_rotated": layers,
+            "split_keys": int(os.environ.get("VO_DECODE_SPLIT", "512")),
+        },
+        "tokens_per_s": round(S / sec, 1),
+        "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        "algorithmic_bytes_per_step": nbytes,
+        "kernels_us": {k: round(v["avg_ms"] * 1e3, 2) for k, v in prof.items()},
+        "ms_per_step_event_timed": round(sec_prof * 1e3, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode_splitk",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": traffic,
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(orc, W, wl, nbytes, args)
+    return line
+
+
+def cpu_baseline(orc, W, wl, nbytes, args):
+    """The oracle (C restatement of the reference's CPU attention, row-parallel
+    like rayon) on the same workload: the whole decode_attention of the step,
+    repeated until about args.cpu_seconds have passed."""
+    model, avail = cpu_info()
+    threads = min(avail, args.cpu_threads)
+    pool = W.oracle_pool(orc, wl)
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    while True:
+        t0 = time.perf_counter()
+        W.oracle_attention(orc, wl, pool=pool, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= 50:
+            break
+    med = float(np.median(times))
+    S = wl.rows
+    return {
+        "value": round(nbytes / med / 1e9, 2),
+        "unit": "GB/s",
+        "tokens_per_s": round(S / med, 2),
+        "ms_per_step": round(med * 1e3, 2),
+        "cores": threads,
+        "kind": "port",
+        "cpu": model,
+        "sample": (f"full decode_attention of the same step ({S} rows, f32 oracle on the bf16 "
+                   f"inputs), median of {len(times)} runs; same algorithmic-byte definition"),
+    }
+
+
+def bench_prefill(vo, W, orc, args):
+    import torch
+    heads, kvh, hd, bs = 32, 8, 128, 16
+    ctx = W.cfg3_context_lens()
+    backend = vo.HipBackend(device=0, max_seqs=8, max_rows=W.FILL_ROWS, max_table_entries=12000,
+                            max_query_heads=heads)
+    wl = W.build(vo, backend, kind="prefill", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=bs, num_blocks=12000, context_lens=ctx, num_new=[512] * 8, seed=3,
+                 keep_host=False)
+    out = torch.empty_like(wl.q)
+
+    def step(i):
+        backend.write_kv(wl.pool, 0, wl.k_new, wl.v_new, wl.meta)
+        backend.prefill_attention(wl.q, wl.pool, 0, wl.meta, out=out)
+
+    sec = time_steps(torch, step, max(3, args.steps // 5), 2)
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    time_steps(torch, step, max(3, args.steps // 5), 0)
+    vo.enable_profiling(False)
+    prof = vo.profile()
+    flops = wl.attention_flops()
+    kern = max(prof.items(), key=lambda kv: kv[1]["total_ms"])
+    k_s = kern[1]["avg_ms"] / 1e3
+    return {
+        "metric": "chunked prefill attention TFLOP/s (causal-aware), Llama-3-8B shape, 1 GPU",
+        "value": round(flops / sec / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg3: 8 seqs x 512-row chunk, ctx U[0,8192] seed 3",
+                   "step": "write_kv + prefill_attention"},
+        "kernels_us": {k: round(v["avg_ms"] * 1e3, 2) for k, v in prof.items()},
+        "roofline": {"bound": "mfma", "kernel": kern[0],
+                     "achieved": round(flops / k_s / 1e12, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(flops / k_s / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=2, help="pool layers to rotate over")
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg5", "all"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build runs "
+              f"the paged-attention path on a single MI355X and has no multi-GPU mode.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    vo = _load_package()
+    import oracle as orc
+    import workloads as W
+
+    lines = []
+    if args.config in ("cfg2", "all"):
+        cfg = dict(name="cfg2: isolated paged decode, Llama-3-8B shape", heads=32,
+                   ctx=W.cfg2_context_lens(), seed=2, num_blocks=20000,
+                   ctx_desc="U[512, 4096], seed 2, keys = ctx + 1")
+        lines.append(bench_decode(vo, W, orc, args, cfg))
+    if args.config in ("cfg5", "all"):
+        cfg = dict(name="cfg5: prefix-shared decode, Llama-3-70B layer shape", heads=64,
+                   ctx=W.cfg5_context_lens(), seed=5, num_blocks=40000, shared_prefix=4096,
+                   shared_count=64,
+                   ctx_desc="64 x (4096 shared + U[256,1024]) + 1 x 32768, seed 5",
+                   metric="prefix-shared decode attn GB/s (logical bytes), Llama-3-70B layer")
+        lines.append(bench_decode(vo, W, orc, args, cfg))
+    if args.config in ("cfg3", "all"):
+        lines.append(bench_prefill(vo, W, orc, args))
+    for line in lines:
+        print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

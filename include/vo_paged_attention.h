@@ -1,0 +1,294 @@
+/*
+ * vo_paged_attention.h -- C ABI of the MI355X (gfx950) paged-attention backend.
+ *
+ * This is the drop-in boundary for vllm-oxide's attention path.  The Rust
+ * engine's `Backend` trait (crates/engine/src/backend/mod.rs:61-182) is
+ * op-level: the engine owns block tables and slot mappings, the backend owns
+ * the KV bytes (mod.rs:10-12).  Each trait op on the attention path has one
+ * entry point here, with the same argument meaning and the same error classes
+ * (crates/engine/src/error.rs:8-56):
+ *
+ *   Backend::alloc_kv_pool   (mod.rs:73-74)   -> vo_kv_pool_create
+ *   Backend::kv_layout       (mod.rs:75)      -> vo_kv_pool_layout
+ *   Backend::write_kv        (mod.rs:107-119) -> vo_write_kv
+ *   Backend::prefill_attention (mod.rs:121-135) -> vo_prefill_attention
+ *   Backend::decode_attention  (mod.rs:137-149) -> vo_decode_attention
+ *   Backend::read            (mod.rs:177-181) -> vo_gather_kv (debug/test only)
+ *
+ * plus the paged-KV addressing of crates/engine/src/backend/paged.rs
+ * (slot_of, PrefillMeta::new, DecodeMeta::new, last_rows) as host functions,
+ * and a device-resident copy of one step's metadata (vo_step_meta) so that
+ * block tables and slot mappings cross host->device once per step, not once
+ * per layer.
+ *
+ * Conventions
+ *  - Every function returns vo_status (0 = VO_OK).  All validation happens on
+ *    the host, before anything is enqueued, exactly as the reference checks
+ *    before it writes (cpu/mod.rs:265-272, attention.rs:130-147,
+ *    arena/ops.rs:191-214, paged.rs:64-80).  On failure nothing is enqueued and
+ *    vo_last_error() describes the error.  No C++ exception crosses the ABI.
+ *  - Activations (queries, keys, values, outputs) are device pointers to
+ *    row-major bf16 matrices, the GPU counterpart of the reference's f32
+ *    workspace `Region {offset, rows, cols}` (mod.rs:31-38).  Accumulation is
+ *    fp32.  Block tables, slots and lengths are host arrays, borrowed for the
+ *    duration of the call only.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Every device op is asynchronous and stream-ordered; no call synchronises
+ *    the device (the reference's one sync per step is argmax, mod.rs:169-175).
+ *  - Safety contract (mod.rs:49-60): device regions are in bounds for the
+ *    shapes given, and an output region overlaps no input region.  The
+ *    library checks the overlap it can see (q vs out) and returns
+ *    VO_ERR_SHAPE.
+ *  - Not thread-safe per object: one engine thread owns a pool and a meta
+ *    (the reference's "one engine thread owns the CUDA context").
+ */
+#ifndef VO_PAGED_ATTENTION_H
+#define VO_PAGED_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Status codes: one per EngineError variant on this path              */
+/* (error.rs:8-56), plus the device and argument classes a C ABI needs. */
+/* ------------------------------------------------------------------ */
+typedef enum vo_status {
+    VO_OK = 0,
+    VO_ERR_SHAPE = 1,                  /* EngineError::Shape            error.rs:11-12 */
+    VO_ERR_CAPACITY = 2,               /* EngineError::Capacity         error.rs:13-18 */
+    VO_ERR_BLOCK_TABLE_TOO_SHORT = 3,  /* EngineError::BlockTable       error.rs:21-22 */
+    VO_ERR_SLOT_OUT_OF_RANGE = 4,      /* EngineError::SlotOutOfRange   error.rs:23-28 */
+    VO_ERR_BLOCK_OUT_OF_RANGE = 5,     /* EngineError::BlockOutOfRange  error.rs:29-34 */
+    VO_ERR_DEVICE = 6,                 /* HIP runtime failure (no reference counterpart) */
+    VO_ERR_INVALID_ARGUMENT = 7,       /* NULL pointer or zero size where one is required */
+    VO_ERR_UNSUPPORTED = 8             /* shape outside what the kernels are built for */
+} vo_status;
+
+/* Detail of the last failed call on the calling thread.  The numeric fields
+ * carry what the reference's error variant carries:
+ *   BlockTableTooShort {op, tokens, needed, have}       (paged.rs:57-62)
+ *   SlotOutOfRange     {op, slot -> value, num_slots -> limit}
+ *   BlockOutOfRange    {op, block -> value, num_blocks -> limit}
+ *   Capacity           {what -> op, need -> value, limit}
+ * `seq` is the sequence index for per-sequence errors.  `message` is the
+ * reference's Display text for the variant. */
+typedef struct vo_error_info {
+    int32_t status;
+    char op[48];
+    uint64_t seq;
+    uint64_t tokens;
+    uint64_t needed;
+    uint64_t have;
+    uint64_t value;
+    uint64_t limit;
+    char message[256];
+} vo_error_info;
+
+/* Fills *out with the last error of this thread and returns its status
+ * (VO_OK if the last call succeeded).  `out` may be NULL. */
+int32_t vo_last_error(vo_error_info *out);
+const char *vo_status_name(int32_t status);
+const char *vo_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Paged-KV addressing, host side (paged.rs)                          */
+/* ------------------------------------------------------------------ */
+
+/* KvLayout (paged.rs:25-45).  Per layer, K and V each hold
+ * num_blocks * block_size slots of kv_heads x head_dim values. */
+typedef struct vo_kv_layout {
+    uint64_t num_layers;
+    uint64_t num_blocks;
+    uint64_t block_size;
+    uint64_t kv_heads;
+    uint64_t head_dim;
+} vo_kv_layout;
+
+/* KvLayout::num_slots (paged.rs:38-40) and ::layer_elems (paged.rs:42-44). */
+uint64_t vo_kv_layout_num_slots(const vo_kv_layout *layout);
+uint64_t vo_kv_layout_layer_elems(const vo_kv_layout *layout);
+
+/* slot_of (paged.rs:48-52): table[pos / bs] * bs + pos % bs.  The reference
+ * panics on an index past the table; here that is VO_ERR_BLOCK_TABLE_TOO_SHORT. */
+int32_t vo_slot_of(const uint32_t *block_table, uint64_t table_len, uint64_t pos,
+                   uint64_t block_size, uint32_t *out_slot);
+
+/* One sequence of a prefill step (PrefillSeq, paged.rs:84-92). */
+typedef struct vo_prefill_seq {
+    uint64_t context_len;
+    uint64_t num_new;
+    const uint32_t *block_table;
+    uint64_t block_table_len;
+} vo_prefill_seq;
+
+/* One sequence of a decode step (DecodeSeq, paged.rs:164-168). */
+typedef struct vo_decode_seq {
+    uint64_t context_len;
+    const uint32_t *block_table;
+    uint64_t block_table_len;
+} vo_decode_seq;
+
+/* PrefillMeta::new (paged.rs:117-143) into caller-sized arrays:
+ * seq_row_starts [S+1]; positions, slot_mapping, row_seq, row_num_keys [T]
+ * with T = sum num_new.  Any output pointer may be NULL.  Fails with
+ * VO_ERR_BLOCK_TABLE_TOO_SHORT {op "prefill", tokens, needed, have, seq}. */
+int32_t vo_prefill_meta_build(const vo_prefill_seq *seqs, uint64_t num_seqs,
+                              uint64_t block_size, uint64_t *seq_row_starts,
+                              uint32_t *positions, uint32_t *slot_mapping,
+                              uint64_t *row_seq, uint64_t *row_num_keys);
+
+/* DecodeMeta::new (paged.rs:189-209): outputs [S].  Fails with
+ * VO_ERR_BLOCK_TABLE_TOO_SHORT {op "decode", ...}. */
+int32_t vo_decode_meta_build(const vo_decode_seq *seqs, uint64_t num_seqs,
+                             uint64_t block_size, uint32_t *positions,
+                             uint32_t *slot_mapping, uint64_t *row_seq,
+                             uint64_t *row_num_keys);
+
+/* PrefillMeta::last_rows (paged.rs:154-159): out[s] = seq_row_starts[s+1]-1. */
+int32_t vo_last_rows(const uint64_t *seq_row_starts, uint64_t num_seqs, uint32_t *out);
+
+/* ------------------------------------------------------------------ */
+/* KV pool (Backend::KvPool, mod.rs:64-75)                             */
+/* ------------------------------------------------------------------ */
+
+/* Opaque.  Device memory for all layers' K and V, bf16, zero-filled at
+ * creation (the reference's calloc, cpu/mod.rs:148-157).  The physical
+ * layout is private to the backend (ADR 0003); logical slot semantics are the
+ * reference's: slot = block * block_size + offset. */
+typedef struct vo_kv_pool vo_kv_pool;
+
+/* Backend::alloc_kv_pool (mod.rs:73-74): allocate once at startup on
+ * `device`.  head_dim must be a multiple of 8; the fast kernels cover
+ * head_dim 64/128 with block_size 16, every other shape runs on the generic
+ * kernels. */
+int32_t vo_kv_pool_create(const vo_kv_layout *layout, int32_t device, vo_kv_pool **out);
+void vo_kv_pool_destroy(vo_kv_pool *pool);
+/* Backend::kv_layout (mod.rs:75). */
+int32_t vo_kv_pool_layout(const vo_kv_pool *pool, vo_kv_layout *out);
+/* Bytes of device memory the pool holds. */
+uint64_t vo_kv_pool_bytes(const vo_kv_pool *pool);
+
+/* ------------------------------------------------------------------ */
+/* Step metadata, device resident                                      */
+/* ------------------------------------------------------------------ */
+
+/* Opaque.  Preallocated at startup for a maximum batch, then refilled once
+ * per step with a PrefillMeta, a DecodeMeta or a bare slot list.  Holds a
+ * host copy for validation and a device copy for the kernels, plus the
+ * split-K work plan and the fp32 partial buffers the decode kernels use.
+ * Nothing is allocated after creation (CLAUDE.md:70 "no allocation in the
+ * hot loop"). */
+typedef struct vo_step_meta vo_step_meta;
+
+/* max_rows: rows (tokens) per step; max_seqs: sequences per step;
+ * max_table_entries: sum of block-table lengths per step; max_query_heads:
+ * the largest num_heads an attention call will use. */
+int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs, uint64_t max_rows,
+                            uint64_t max_table_entries, uint64_t max_query_heads,
+                            vo_step_meta **out);
+void vo_step_meta_destroy(vo_step_meta *meta);
+
+/* Upload a PrefillMeta (paged.rs:97-114) built by vo_prefill_meta_build or by
+ * the engine.  Tables are CSR: table s is tables[table_off[s] ..
+ * table_off[s+1]).  Fails with VO_ERR_CAPACITY when the batch exceeds the
+ * sizes given at creation.  Enqueues host->device copies on `stream`; the
+ * host arrays may be reused as soon as the call returns. */
+int32_t vo_step_meta_upload_prefill(vo_step_meta *meta, uint64_t block_size, uint64_t num_seqs,
+                                    const uint64_t *table_off, const uint32_t *tables,
+                                    const uint64_t *context_lens,
+                                    const uint64_t *seq_row_starts, uint64_t num_rows,
+                                    const uint32_t *positions, const uint32_t *slot_mapping,
+                                    const uint64_t *row_seq, const uint64_t *row_num_keys,
+                                    void *stream);
+
+/* Upload a DecodeMeta (paged.rs:173-186): one row per sequence. */
+int32_t vo_step_meta_upload_decode(vo_step_meta *meta, uint64_t block_size, uint64_t num_seqs,
+                                   const uint64_t *table_off, const uint32_t *tables,
+                                   const uint32_t *positions, const uint32_t *slot_mapping,
+                                   const uint64_t *row_seq, const uint64_t *row_num_keys,
+                                   void *stream);
+
+/* Upload only a slot list, for write_kv calls whose slots are not a step's
+ * slot mapping (the reference's tests write ad-hoc ranges, cpu/tests.rs:210-230). */
+int32_t vo_step_meta_upload_slots(vo_step_meta *meta, const uint32_t *slots, uint64_t num_slots,
+                                  void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Ops                                                                 */
+/* ------------------------------------------------------------------ */
+
+/* Backend::write_kv (mod.rs:107-119; CPU: cpu/mod.rs:257-285) -- the
+ * reshape_and_cache kernel.  Stores row t of keys/values ([rows, cols] bf16,
+ * cols = kv_heads * head_dim) at slot slot_mapping[t] of `layer`, where the
+ * slot mapping is the one last uploaded into `meta`.  Checks first, as
+ * arena/ops.rs:102-131 and cpu/mod.rs:265-272 do: rows == number of slots,
+ * cols == kv_heads * head_dim, layer < num_layers (VO_ERR_SHAPE), then every
+ * slot < num_slots (VO_ERR_SLOT_OUT_OF_RANGE).  Slots must be distinct within
+ * one call: the reference's "later row wins" (cpu/mod.rs:277-283) has no
+ * ordering guarantee on a GPU. */
+int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys, const void *values,
+                    uint64_t rows, uint64_t cols, const vo_step_meta *meta, void *stream);
+
+/* Backend::prefill_attention (mod.rs:121-135; CPU: cpu/mod.rs:287-312).
+ * queries, out: [rows, num_heads * head_dim] bf16 with num_heads = cols /
+ * head_dim.  Row t attends to row_num_keys[t] keys of sequence row_seq[t]
+ * through its block table; causality comes from the key counts
+ * (attention.rs:16).  Checks: arena/ops.rs:191-214 (VO_ERR_SHAPE), then
+ * every table entry < num_blocks (VO_ERR_BLOCK_OUT_OF_RANGE,
+ * attention.rs:130-147).  `meta` must hold a prefill upload. */
+int32_t vo_prefill_attention(const void *queries, uint64_t rows, uint64_t cols,
+                             const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *meta,
+                             void *out, void *stream);
+
+/* Backend::decode_attention (mod.rs:137-149; CPU: cpu/mod.rs:314-339): one
+ * query row per sequence.  Split-K over the keys with an fp32 partial per
+ * split and a reduce kernel.  `meta` must hold a decode upload. */
+int32_t vo_decode_attention(const void *queries, uint64_t rows, uint64_t cols,
+                            const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *meta,
+                            void *out, void *stream);
+
+/* Debug and test only (the counterpart of Backend::read, mod.rs:177-181):
+ * gather keys 0..num_keys of sequence `seq` of the last upload in `meta` from
+ * `layer` into out_keys and out_values, each [num_keys, kv_heads * head_dim]
+ * bf16 in the reference's logical layout (paged.rs:25-28): row j is the
+ * pool entry at slot_of(table, j).  The kernel reads the block table from
+ * the meta's device copy, as the attention kernels do.  Checks seq range
+ * (VO_ERR_SHAPE), coverage (VO_ERR_BLOCK_TABLE_TOO_SHORT) and block range
+ * (VO_ERR_BLOCK_OUT_OF_RANGE) first. */
+int32_t vo_gather_kv(const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *meta,
+                     uint64_t seq, uint64_t num_keys, void *out_keys, void *out_values,
+                     void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Opt-in kernel timing (the reference's opt-in per-op timing,         */
+/* arena.rs:82-87 OpStat, :129-136 enable_profiling)                   */
+/* ------------------------------------------------------------------ */
+
+/* Per-kernel totals since the last reset. */
+typedef struct vo_kernel_stat {
+    char name[48];
+    uint64_t calls;
+    double total_ms;
+    double min_ms;
+    double max_ms;
+} vo_kernel_stat;
+
+/* While enabled, every kernel launch is bracketed by HIP events on its
+ * stream.  Recording never waits on the device. */
+int32_t vo_profiling_enable(int32_t on);
+/* Waits for the recorded events (call outside the hot loop), folds them into
+ * the per-kernel totals and copies up to `capacity` entries to `out`;
+ * `*count` receives the number of kernels seen. */
+int32_t vo_profile_read(vo_kernel_stat *out, uint64_t capacity, uint64_t *count);
+/* Drops all totals and pending events. */
+void vo_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VO_PAGED_ATTENTION_H */

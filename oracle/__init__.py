@@ -1,0 +1,277 @@
+"""CPU oracle for the paged-attention path -- TEST INFRASTRUCTURE ONLY.
+
+numpy wrappers over ``oracle/build/libvo_oracle_v{3,4}.so`` (built from
+``vo_oracle.c`` by ``oracle/Makefile``), the C restatement of the reference's
+CPU backend and paged metadata (citations in vo_oracle.h / vo_oracle.c).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg may
+import this module, and only as the checker or the timed CPU baseline.  The
+product library never calls it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+from typing import List, Sequence, Tuple
+
+import numpy as np
+
+_HERE = pathlib.Path(__file__).resolve().parent
+
+
+def _has_avx512() -> bool:
+    try:
+        flags = pathlib.Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl"))
+
+
+VARIANT = "v4" if _has_avx512() else "v3"
+LIB_PATH = _HERE / "build" / f"libvo_oracle_{VARIANT}.so"
+
+_u64 = ctypes.c_uint64
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+OK = 0
+BLOCK_TABLE_TOO_SHORT = 3
+SLOT_OUT_OF_RANGE = 4
+BLOCK_OUT_OF_RANGE = 5
+
+
+class Err(ctypes.Structure):
+    _fields_ = [("seq", _u64), ("tokens", _u64), ("needed", _u64), ("have", _u64),
+                ("value", _u64), ("limit", _u64)]
+
+
+class OracleError(Exception):
+    def __init__(self, code: int, err: Err):
+        self.code = code
+        self.seq, self.tokens, self.needed = int(err.seq), int(err.tokens), int(err.needed)
+        self.have, self.value, self.limit = int(err.have), int(err.value), int(err.limit)
+        super().__init__(f"oracle error {code}: seq {self.seq} tokens {self.tokens} "
+                         f"needed {self.needed} have {self.have} value {self.value} "
+                         f"limit {self.limit}")
+
+
+def _load():
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH} missing: run `make -C oracle`")
+    h = ctypes.CDLL(str(LIB_PATH))
+    sig = {
+        "vo_oracle_rand_vec": (None, [_u64, _u64, _f32p]),
+        "vo_oracle_max_rel_diff": (ctypes.c_float, [_f32p, _f32p, _u64]),
+        "vo_oracle_slot_of": (ctypes.c_uint32, [_u32p, _u64, _u64]),
+        "vo_oracle_check_covers": (ctypes.c_int, [_u64, _u64, _u64, ctypes.POINTER(Err)]),
+        "vo_oracle_prefill_meta": (ctypes.c_int, [_u64, _u64p, _u64p, _u64p, _u32p, _u64,
+                                                  _u64p, _u32p, _u32p, _u64p, _u64p,
+                                                  ctypes.POINTER(Err)]),
+        "vo_oracle_last_rows": (None, [_u64p, _u64, _u32p]),
+        "vo_oracle_decode_meta": (ctypes.c_int, [_u64, _u64p, _u64p, _u32p, _u64, _u32p, _u32p,
+                                                 _u64p, _u64p, ctypes.POINTER(Err)]),
+        "vo_oracle_dot": (ctypes.c_float, [_f32p, _f32p, _u64]),
+        "vo_oracle_write_kv": (ctypes.c_int, [_f32p, _f32p, _u64, _u64, _f32p, _f32p, _u32p,
+                                              _u64, ctypes.POINTER(Err)]),
+        "vo_oracle_check_block_tables": (ctypes.c_int, [_u64, _u64p, _u32p, _u64,
+                                                        ctypes.POINTER(Err)]),
+        "vo_oracle_paged_attention": (None, [_f32p, _f32p, _f32p, _f32p, _u64, _u64, _u64, _u64,
+                                             _u64p, _u32p, _u64p, _u64p, _u64, ctypes.c_int]),
+        "vo_oracle_naive_attend_f64": (None, [_f32p, _f32p, _f32p, _u64, _u64, _u64, _u64,
+                                              _f32p]),
+        "vo_oracle_splitk_combine": (None, [_u64, _u64, _f32p, _f32p, _f32p, _f32p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    return h
+
+
+lib = _load()
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def _u64a(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint64))
+
+
+def _pf(a):
+    return a.ctypes.data_as(_f32p)
+
+
+def _p32(a):
+    return a.ctypes.data_as(_u32p)
+
+
+def _p64(a):
+    return a.ctypes.data_as(_u64p)
+
+
+def csr(tables: Sequence[Sequence[int]]) -> Tuple[np.ndarray, np.ndarray]:
+    off = np.zeros(len(tables) + 1, np.uint64)
+    if len(tables):
+        off[1:] = np.cumsum([len(t) for t in tables])
+    flat = np.concatenate([_u32(t) for t in tables]) if len(tables) and off[-1] else np.zeros(1, np.uint32)
+    return off, _u32(flat)
+
+
+# ---- testutil.rs ----------------------------------------------------------
+
+def rand_vec(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(max(n, 1), np.float32)
+    lib.vo_oracle_rand_vec(seed, n, _pf(out))
+    return out[:n]
+
+
+def max_rel_diff(a, b) -> float:
+    a, b = _f32(a).ravel(), _f32(b).ravel()
+    assert a.shape == b.shape
+    return float(lib.vo_oracle_max_rel_diff(_pf(a), _pf(b), a.size))
+
+
+# ---- paged.rs -------------------------------------------------------------
+
+def slot_of(table, pos: int, block_size: int) -> int:
+    t = _u32(table)
+    return int(lib.vo_oracle_slot_of(_p32(t), pos, block_size))
+
+
+def prefill_meta(seqs: Sequence[Tuple[int, int, Sequence[int]]], block_size: int) -> dict:
+    """seqs = [(context_len, num_new, table)] -> PrefillMeta fields."""
+    ctx = _u64a([s[0] for s in seqs])
+    new = _u64a([s[1] for s in seqs])
+    off, flat = csr([s[2] for s in seqs])
+    T = int(new.sum()) if len(seqs) else 0
+    starts = np.zeros(len(seqs) + 1, np.uint64)
+    pos = np.zeros(max(T, 1), np.uint32)
+    slots = np.zeros(max(T, 1), np.uint32)
+    rseq = np.zeros(max(T, 1), np.uint64)
+    rkeys = np.zeros(max(T, 1), np.uint64)
+    err = Err()
+    rc = lib.vo_oracle_prefill_meta(len(seqs), _p64(ctx if len(seqs) else np.zeros(1, np.uint64)),
+                                    _p64(new if len(seqs) else np.zeros(1, np.uint64)), _p64(off),
+                                    _p32(flat), block_size, _p64(starts), _p32(pos), _p32(slots),
+                                    _p64(rseq), _p64(rkeys), ctypes.byref(err))
+    if rc != OK:
+        raise OracleError(rc, err)
+    last = np.zeros(max(len(seqs), 1), np.uint32)
+    lib.vo_oracle_last_rows(_p64(starts), len(seqs), _p32(last))
+    return dict(seq_row_starts=starts, positions=pos[:T], slot_mapping=slots[:T],
+                row_seq=rseq[:T], row_num_keys=rkeys[:T], last_rows=last[:len(seqs)],
+                table_off=off, tables=flat, context_lens=ctx)
+
+
+def decode_meta(seqs: Sequence[Tuple[int, Sequence[int]]], block_size: int) -> dict:
+    """seqs = [(context_len, table)] -> DecodeMeta fields."""
+    n = len(seqs)
+    ctx = _u64a([s[0] for s in seqs]) if n else np.zeros(1, np.uint64)
+    off, flat = csr([s[1] for s in seqs])
+    pos = np.zeros(max(n, 1), np.uint32)
+    slots = np.zeros(max(n, 1), np.uint32)
+    rseq = np.zeros(max(n, 1), np.uint64)
+    rkeys = np.zeros(max(n, 1), np.uint64)
+    err = Err()
+    rc = lib.vo_oracle_decode_meta(n, _p64(ctx), _p64(off), _p32(flat), block_size, _p32(pos),
+                                   _p32(slots), _p64(rseq), _p64(rkeys), ctypes.byref(err))
+    if rc != OK:
+        raise OracleError(rc, err)
+    return dict(positions=pos[:n], slot_mapping=slots[:n], row_seq=rseq[:n],
+                row_num_keys=rkeys[:n], table_off=off, tables=flat)
+
+
+# ---- cpu/mod.rs, cpu/attention.rs -------------------------------------------
+
+def dot(a, b) -> float:
+    a, b = _f32(a), _f32(b)
+    return float(lib.vo_oracle_dot(_pf(a), _pf(b), a.size))
+
+
+class Pool:
+    """CpuKvPool (cpu/mod.rs:31-37): f32 [layers][num_slots, kv_heads*head_dim]."""
+
+    def __init__(self, num_layers, num_blocks, block_size, kv_heads, head_dim):
+        self.num_layers, self.num_blocks, self.block_size = num_layers, num_blocks, block_size
+        self.kv_heads, self.head_dim = kv_heads, head_dim
+        self.num_slots = num_blocks * block_size
+        w = kv_heads * head_dim
+        self.keys = [np.zeros((self.num_slots, w), np.float32) for _ in range(num_layers)]
+        self.values = [np.zeros((self.num_slots, w), np.float32) for _ in range(num_layers)]
+
+    def write_kv(self, layer, keys, values, slots) -> None:
+        k, v, s = _f32(keys), _f32(values), _u32(slots)
+        err = Err()
+        rc = lib.vo_oracle_write_kv(_pf(self.keys[layer]), _pf(self.values[layer]),
+                                    self.num_slots, self.kv_heads * self.head_dim, _pf(k), _pf(v),
+                                    _p32(s), len(s), ctypes.byref(err))
+        if rc != OK:
+            raise OracleError(rc, err)
+
+    def check_block_tables(self, tables) -> None:
+        off, flat = csr(tables)
+        err = Err()
+        rc = lib.vo_oracle_check_block_tables(len(tables), _p64(off), _p32(flat),
+                                              self.num_blocks, ctypes.byref(err))
+        if rc != OK:
+            raise OracleError(rc, err)
+
+    def attention(self, queries, layer, tables, row_seq, row_num_keys, threads=None):
+        """prefill_attention / decode_attention (cpu/mod.rs:287-339)."""
+        self.check_block_tables(tables)
+        q = _f32(queries)
+        rows = q.shape[0]
+        out = np.zeros_like(q)
+        off, flat = csr(tables)
+        rs, rk = _u64a(row_seq), _u64a(row_num_keys)
+        num_heads = q.shape[1] // self.head_dim
+        if threads is None:
+            threads = os.cpu_count() or 1
+        lib.vo_oracle_paged_attention(_pf(q), _pf(out), _pf(self.keys[layer]),
+                                      _pf(self.values[layer]), num_heads, self.kv_heads,
+                                      self.head_dim, self.block_size, _p64(off), _p32(flat),
+                                      _p64(rs if rows else np.zeros(1, np.uint64)),
+                                      _p64(rk if rows else np.zeros(1, np.uint64)), rows,
+                                      int(threads))
+        return out
+
+
+def paged_attention_raw(queries, pool_k, pool_v, num_kv_heads, head_dim, block_size, table_off,
+                        tables, row_seq, row_num_keys, threads=None) -> np.ndarray:
+    """attention.rs:44-128 on caller-owned arrays (pool_k/pool_v: [slots, kvh*hd] f32)."""
+    q = _f32(queries)
+    out = np.zeros_like(q)
+    rows = q.shape[0]
+    if threads is None:
+        threads = os.cpu_count() or 1
+    lib.vo_oracle_paged_attention(_pf(q), _pf(out), _pf(pool_k), _pf(pool_v),
+                                  q.shape[1] // head_dim, num_kv_heads, head_dim, block_size,
+                                  _p64(_u64a(table_off)), _p32(_u32(tables)),
+                                  _p64(_u64a(row_seq)), _p64(_u64a(row_num_keys)), rows,
+                                  int(threads))
+    return out
+
+
+def naive_attend_f64(q, seq_k, seq_v, pos, num_heads, num_kv_heads, head_dim) -> np.ndarray:
+    """cpu/tests.rs:184-208."""
+    q, k, v = _f32(q), _f32(seq_k), _f32(seq_v)
+    out = np.zeros(num_heads * head_dim, np.float32)
+    lib.vo_oracle_naive_attend_f64(_pf(q), _pf(k), _pf(v), pos, num_heads, num_kv_heads,
+                                   head_dim, _pf(out))
+    return out
+
+
+def splitk_combine(m, l, acc) -> np.ndarray:
+    m, l, acc = _f32(m), _f32(l), _f32(acc)
+    hd = acc.shape[-1]
+    out = np.zeros(hd, np.float32)
+    lib.vo_oracle_splitk_combine(len(m), hd, _pf(m), _pf(l), _pf(acc), _pf(out))
+    return out

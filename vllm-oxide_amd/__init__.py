@@ -1,0 +1,554 @@
+"""vllm-oxide paged attention for MI355X (gfx950).
+
+Python view of ``libvo_paged_attention.so`` (C ABI in
+``include/vo_paged_attention.h``).  The names and argument meanings mirror the
+reference engine's Rust interface:
+
+* ``KvLayout``, ``slot_of``, ``PrefillSeq``/``PrefillMeta.new``,
+  ``DecodeSeq``/``DecodeMeta.new``, ``last_rows`` --
+  crates/engine/src/backend/paged.rs:25-209
+* ``HipBackend.alloc_kv_pool``, ``kv_layout``, ``write_kv``,
+  ``prefill_attention``, ``decode_attention``, ``read_kv`` --
+  the attention-path ops of ``trait Backend``,
+  crates/engine/src/backend/mod.rs:61-182
+* ``EngineError`` and its subclasses -- crates/engine/src/error.rs:8-56
+
+All compute runs in the HIP library.  Importing this package loads the
+library and raises ``ImportError`` when it is missing; there is no CPU path.
+torch is used only for device memory and streams.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+__all__ = [
+    "LIB_PATH", "lib", "KvLayout", "slot_of", "PrefillSeq", "PrefillMeta", "DecodeSeq",
+    "DecodeMeta", "EngineError", "ShapeError", "CapacityError", "BlockTableTooShort",
+    "SlotOutOfRange", "BlockOutOfRange", "DeviceError", "InvalidArgument", "Unsupported",
+    "HipBackend", "KvPool", "StepMeta",
+]
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = pathlib.Path(os.environ.get("VO_LIB_PATH", _HERE / "libvo_paged_attention.so"))
+
+# ---------------------------------------------------------------------------
+# C ABI
+# ---------------------------------------------------------------------------
+VO_OK = 0
+VO_ERR_SHAPE = 1
+VO_ERR_CAPACITY = 2
+VO_ERR_BLOCK_TABLE_TOO_SHORT = 3
+VO_ERR_SLOT_OUT_OF_RANGE = 4
+VO_ERR_BLOCK_OUT_OF_RANGE = 5
+VO_ERR_DEVICE = 6
+VO_ERR_INVALID_ARGUMENT = 7
+VO_ERR_UNSUPPORTED = 8
+
+_u64 = ctypes.c_uint64
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_vp = ctypes.c_void_p
+
+
+class vo_error_info(ctypes.Structure):
+    _fields_ = [
+        ("status", ctypes.c_int32), ("op", ctypes.c_char * 48), ("seq", _u64),
+        ("tokens", _u64), ("needed", _u64), ("have", _u64), ("value", _u64),
+        ("limit", _u64), ("message", ctypes.c_char * 256),
+    ]
+
+
+class vo_kv_layout(ctypes.Structure):
+    _fields_ = [("num_layers", _u64), ("num_blocks", _u64), ("block_size", _u64),
+                ("kv_heads", _u64), ("head_dim", _u64)]
+
+
+class vo_kernel_stat(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 48), ("calls", _u64), ("total_ms", ctypes.c_double),
+                ("min_ms", ctypes.c_double), ("max_ms", ctypes.c_double)]
+
+
+class vo_prefill_seq(ctypes.Structure):
+    _fields_ = [("context_len", _u64), ("num_new", _u64), ("block_table", _u32p),
+                ("block_table_len", _u64)]
+
+
+class vo_decode_seq(ctypes.Structure):
+    _fields_ = [("context_len", _u64), ("block_table", _u32p), ("block_table_len", _u64)]
+
+
+# Every exported symbol of the C ABI with its ctypes signature.
+SIGNATURES = {
+    "vo_last_error": (ctypes.c_int32, [ctypes.POINTER(vo_error_info)]),
+    "vo_status_name": (ctypes.c_char_p, [ctypes.c_int32]),
+    "vo_version": (ctypes.c_char_p, []),
+    "vo_kv_layout_num_slots": (_u64, [ctypes.POINTER(vo_kv_layout)]),
+    "vo_kv_layout_layer_elems": (_u64, [ctypes.POINTER(vo_kv_layout)]),
+    "vo_slot_of": (ctypes.c_int32, [_u32p, _u64, _u64, _u64, _u32p]),
+    "vo_prefill_meta_build": (ctypes.c_int32, [ctypes.POINTER(vo_prefill_seq), _u64, _u64,
+                                               _u64p, _u32p, _u32p, _u64p, _u64p]),
+    "vo_decode_meta_build": (ctypes.c_int32, [ctypes.POINTER(vo_decode_seq), _u64, _u64,
+                                              _u32p, _u32p, _u64p, _u64p]),
+    "vo_last_rows": (ctypes.c_int32, [_u64p, _u64, _u32p]),
+    "vo_kv_pool_create": (ctypes.c_int32, [ctypes.POINTER(vo_kv_layout), ctypes.c_int32,
+                                           ctypes.POINTER(_vp)]),
+    "vo_kv_pool_destroy": (None, [_vp]),
+    "vo_kv_pool_layout": (ctypes.c_int32, [_vp, ctypes.POINTER(vo_kv_layout)]),
+    "vo_kv_pool_bytes": (_u64, [_vp]),
+    "vo_step_meta_create": (ctypes.c_int32, [_vp, _u64, _u64, _u64, _u64, ctypes.POINTER(_vp)]),
+    "vo_step_meta_destroy": (None, [_vp]),
+    "vo_step_meta_upload_prefill": (ctypes.c_int32, [_vp, _u64, _u64, _u64p, _u32p, _u64p,
+                                                     _u64p, _u64, _u32p, _u32p, _u64p, _u64p,
+                                                     _vp]),
+    "vo_step_meta_upload_decode": (ctypes.c_int32, [_vp, _u64, _u64, _u64p, _u32p, _u32p,
+                                                    _u32p, _u64p, _u64p, _vp]),
+    "vo_step_meta_upload_slots": (ctypes.c_int32, [_vp, _u32p, _u64, _vp]),
+    "vo_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _vp, _vp]),
+    "vo_prefill_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
+    "vo_decode_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
+    "vo_gather_kv": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _vp, _vp, _vp]),
+    "vo_profiling_enable": (ctypes.c_int32, [ctypes.c_int32]),
+    "vo_profile_read": (ctypes.c_int32, [ctypes.POINTER(vo_kernel_stat), _u64, _u64p]),
+    "vo_profile_reset": (None, []),
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            f"g.build()'` (make -C vllm-oxide_amd/csrc).  There is no fallback path.")
+    handle = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    return handle
+
+
+lib = _load()
+
+# ---------------------------------------------------------------------------
+# Errors (error.rs:8-56)
+# ---------------------------------------------------------------------------
+
+
+class EngineError(Exception):
+    """A failed C-ABI call; fields are the reference variant's fields."""
+
+    def __init__(self, info: vo_error_info):
+        self.status = int(info.status)
+        self.op = info.op.decode()
+        self.seq = int(info.seq)
+        self.tokens = int(info.tokens)
+        self.needed = int(info.needed)
+        self.have = int(info.have)
+        self.value = int(info.value)
+        self.limit = int(info.limit)
+        self.message = info.message.decode()
+        super().__init__(f"{lib.vo_status_name(self.status).decode()}: {self.message}")
+
+
+class ShapeError(EngineError): pass
+class CapacityError(EngineError): pass
+class BlockTableTooShort(EngineError): pass
+class SlotOutOfRange(EngineError): pass
+class BlockOutOfRange(EngineError): pass
+class DeviceError(EngineError): pass
+class InvalidArgument(EngineError): pass
+class Unsupported(EngineError): pass
+
+
+_ERROR_CLASSES = {
+    VO_ERR_SHAPE: ShapeError, VO_ERR_CAPACITY: CapacityError,
+    VO_ERR_BLOCK_TABLE_TOO_SHORT: BlockTableTooShort, VO_ERR_SLOT_OUT_OF_RANGE: SlotOutOfRange,
+    VO_ERR_BLOCK_OUT_OF_RANGE: BlockOutOfRange, VO_ERR_DEVICE: DeviceError,
+    VO_ERR_INVALID_ARGUMENT: InvalidArgument, VO_ERR_UNSUPPORTED: Unsupported,
+}
+
+
+def _check(rc: int) -> None:
+    if rc != VO_OK:
+        info = vo_error_info()
+        lib.vo_last_error(ctypes.byref(info))
+        raise _ERROR_CLASSES.get(rc, EngineError)(info)
+
+
+def _u32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def _u64a(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint64))
+
+
+def _p32(a: np.ndarray):
+    return a.ctypes.data_as(_u32p)
+
+
+def _p64(a: np.ndarray):
+    return a.ctypes.data_as(_u64p)
+
+
+# ---------------------------------------------------------------------------
+# paged.rs
+# ---------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class KvLayout:
+    """paged.rs:25-45."""
+    num_layers: int
+    num_blocks: int
+    block_size: int
+    kv_heads: int
+    head_dim: int
+
+    def _c(self) -> vo_kv_layout:
+        return vo_kv_layout(self.num_layers, self.num_blocks, self.block_size, self.kv_heads,
+                            self.head_dim)
+
+    def num_slots(self) -> int:
+        return int(lib.vo_kv_layout_num_slots(ctypes.byref(self._c())))
+
+    def layer_elems(self) -> int:
+        return int(lib.vo_kv_layout_layer_elems(ctypes.byref(self._c())))
+
+
+def slot_of(block_table: Sequence[int], pos: int, block_size: int) -> int:
+    """paged.rs:48-52."""
+    t = _u32(block_table)
+    out = ctypes.c_uint32()
+    _check(lib.vo_slot_of(_p32(t), len(t), pos, block_size, ctypes.byref(out)))
+    return int(out.value)
+
+
+@dataclass
+class PrefillSeq:
+    """paged.rs:84-92."""
+    context_len: int
+    num_new: int
+    block_table: Sequence[int]
+
+
+@dataclass
+class DecodeSeq:
+    """paged.rs:164-168."""
+    context_len: int
+    block_table: Sequence[int]
+
+
+def _csr(tables: List[np.ndarray]):
+    off = np.zeros(len(tables) + 1, dtype=np.uint64)
+    if tables:
+        off[1:] = np.cumsum([len(t) for t in tables])
+    flat = np.concatenate(tables).astype(np.uint32) if tables and off[-1] else np.zeros(1, np.uint32)
+    return off, flat
+
+
+@dataclass
+class PrefillMeta:
+    """paged.rs:97-114, built by the library's PrefillMeta::new restatement."""
+    block_size: int
+    block_tables: List[np.ndarray]
+    context_lens: np.ndarray
+    seq_row_starts: np.ndarray
+    positions: np.ndarray
+    slot_mapping: np.ndarray
+    row_seq: np.ndarray
+    row_num_keys: np.ndarray
+    kind: str = field(default="prefill", repr=False)
+
+    @staticmethod
+    def new(seqs: Sequence[PrefillSeq], block_size: int) -> "PrefillMeta":
+        tables = [_u32(s.block_table) for s in seqs]
+        cseqs = (vo_prefill_seq * max(len(seqs), 1))()
+        for i, (s, t) in enumerate(zip(seqs, tables)):
+            cseqs[i] = vo_prefill_seq(s.context_len, s.num_new, _p32(t), len(t))
+        rows = int(sum(s.num_new for s in seqs))
+        starts = np.zeros(len(seqs) + 1, np.uint64)
+        pos = np.zeros(max(rows, 1), np.uint32)
+        slots = np.zeros(max(rows, 1), np.uint32)
+        rseq = np.zeros(max(rows, 1), np.uint64)
+        rkeys = np.zeros(max(rows, 1), np.uint64)
+        _check(lib.vo_prefill_meta_build(cseqs, len(seqs), block_size, _p64(starts), _p32(pos),
+                                         _p32(slots), _p64(rseq), _p64(rkeys)))
+        return PrefillMeta(block_size, tables,
+                           np.array([s.context_len for s in seqs], np.uint64), starts,
+                           pos[:rows], slots[:rows], rseq[:rows], rkeys[:rows])
+
+    def num_seqs(self) -> int:
+        return len(self.context_lens)
+
+    def num_rows(self) -> int:
+        return len(self.positions)
+
+    def last_rows(self) -> np.ndarray:
+        """paged.rs:154-159."""
+        out = np.zeros(max(self.num_seqs(), 1), np.uint32)
+        starts = _u64a(self.seq_row_starts)
+        _check(lib.vo_last_rows(_p64(starts), self.num_seqs(), _p32(out)))
+        return out[: self.num_seqs()]
+
+
+@dataclass
+class DecodeMeta:
+    """paged.rs:173-186, built by the library's DecodeMeta::new restatement."""
+    block_size: int
+    block_tables: List[np.ndarray]
+    positions: np.ndarray
+    slot_mapping: np.ndarray
+    row_seq: np.ndarray
+    row_num_keys: np.ndarray
+    kind: str = field(default="decode", repr=False)
+
+    @staticmethod
+    def new(seqs: Sequence[DecodeSeq], block_size: int) -> "DecodeMeta":
+        tables = [_u32(s.block_table) for s in seqs]
+        cseqs = (vo_decode_seq * max(len(seqs), 1))()
+        for i, (s, t) in enumerate(zip(seqs, tables)):
+            cseqs[i] = vo_decode_seq(s.context_len, _p32(t), len(t))
+        n = len(seqs)
+        pos = np.zeros(max(n, 1), np.uint32)
+        slots = np.zeros(max(n, 1), np.uint32)
+        rseq = np.zeros(max(n, 1), np.uint64)
+        rkeys = np.zeros(max(n, 1), np.uint64)
+        _check(lib.vo_decode_meta_build(cseqs, n, block_size, _p32(pos), _p32(slots), _p64(rseq),
+                                        _p64(rkeys)))
+        return DecodeMeta(block_size, tables, pos[:n], slots[:n], rseq[:n], rkeys[:n])
+
+    def num_seqs(self) -> int:
+        return len(self.positions)
+
+
+# ---------------------------------------------------------------------------
+# Opt-in kernel timing (arena.rs:129-136 enable_profiling / profile)
+# ---------------------------------------------------------------------------
+
+
+def enable_profiling(on: bool = True) -> None:
+    _check(lib.vo_profiling_enable(1 if on else 0))
+
+
+def profile() -> dict:
+    """{kernel: {"calls", "total_ms", "min_ms", "max_ms", "avg_ms"}}; waits for
+    the recorded events."""
+    n = ctypes.c_uint64()
+    _check(lib.vo_profile_read(None, 0, ctypes.byref(n)))
+    arr = (vo_kernel_stat * max(n.value, 1))()
+    _check(lib.vo_profile_read(arr, n.value, ctypes.byref(n)))
+    out = {}
+    for i in range(n.value):
+        s = arr[i]
+        out[s.name.decode()] = dict(calls=int(s.calls), total_ms=s.total_ms, min_ms=s.min_ms,
+                                    max_ms=s.max_ms,
+                                    avg_ms=s.total_ms / s.calls if s.calls else 0.0)
+    return out
+
+
+def profile_reset() -> None:
+    lib.vo_profile_reset()
+
+
+# ---------------------------------------------------------------------------
+# Backend (mod.rs:61-182, attention path)
+# ---------------------------------------------------------------------------
+
+
+class KvPool:
+    """Backend::KvPool: an opaque device pool (bf16)."""
+
+    def __init__(self, layout: KvLayout, device: int):
+        self.layout = layout
+        self.device = device
+        self._h = _vp()
+        _check(lib.vo_kv_pool_create(ctypes.byref(layout._c()), device, ctypes.byref(self._h)))
+
+    @property
+    def handle(self):
+        return self._h
+
+    def nbytes(self) -> int:
+        return int(lib.vo_kv_pool_bytes(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_kv_pool_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class StepMeta:
+    """Device-resident step metadata (vo_step_meta)."""
+
+    def __init__(self, pool: KvPool, max_seqs: int, max_rows: int, max_table_entries: int,
+                 max_query_heads: int):
+        self._h = _vp()
+        _check(lib.vo_step_meta_create(pool.handle, max_seqs, max_rows, max_table_entries,
+                                       max_query_heads, ctypes.byref(self._h)))
+        self.capacity = (max_seqs, max_rows, max_table_entries, max_query_heads)
+        self.holds = None  # the host meta object last uploaded
+
+    @property
+    def handle(self):
+        return self._h
+
+    def upload(self, meta, stream=None) -> None:
+        off, flat = _csr(meta.block_tables)
+        if isinstance(meta, PrefillMeta):
+            ctx = _u64a(meta.context_lens)
+            starts = _u64a(meta.seq_row_starts)
+            pos = _u32(meta.positions)
+            slots = _u32(meta.slot_mapping)
+            rseq = _u64a(meta.row_seq)
+            rkeys = _u64a(meta.row_num_keys)
+            _check(lib.vo_step_meta_upload_prefill(
+                self._h, meta.block_size, meta.num_seqs(), _p64(off), _p32(flat), _p64(ctx),
+                _p64(starts), meta.num_rows(), _p32(pos), _p32(slots), _p64(rseq), _p64(rkeys),
+                _stream_ptr(stream)))
+        elif isinstance(meta, DecodeMeta):
+            pos = _u32(meta.positions)
+            slots = _u32(meta.slot_mapping)
+            rseq = _u64a(meta.row_seq)
+            rkeys = _u64a(meta.row_num_keys)
+            _check(lib.vo_step_meta_upload_decode(
+                self._h, meta.block_size, meta.num_seqs(), _p64(off), _p32(flat), _p32(pos),
+                _p32(slots), _p64(rseq), _p64(rkeys), _stream_ptr(stream)))
+        else:
+            raise TypeError(f"cannot upload {type(meta).__name__}")
+        self.holds = meta
+
+    def upload_slots(self, slots, stream=None) -> None:
+        s = _u32(slots)
+        _check(lib.vo_step_meta_upload_slots(self._h, _p32(s), len(s), _stream_ptr(stream)))
+        self.holds = None
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_step_meta_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        import torch
+        return _vp(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return _vp(stream)
+    return _vp(stream.cuda_stream)
+
+
+def _dev_ptr(t) -> _vp:
+    import torch
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError("expected a device tensor")
+    if t.dtype != torch.bfloat16 or not t.is_contiguous():
+        raise TypeError("expected a contiguous bfloat16 tensor")
+    return _vp(t.data_ptr())
+
+
+class HipBackend:
+    """The attention-path ops of ``trait Backend`` (mod.rs:61-182) on one GPU.
+
+    Activations are contiguous ``torch.bfloat16`` device tensors (the GPU
+    counterpart of the reference's f32 workspace regions).  Block tables and
+    slot mappings come from ``PrefillMeta``/``DecodeMeta``; the backend uploads
+    a meta to its device-resident copy the first time it sees it, so a step's
+    metadata crosses to the device once for all layers.
+    """
+
+    def __init__(self, device: int = 0, max_seqs: int = 512, max_rows: int = 8192,
+                 max_table_entries: int = 1 << 16, max_query_heads: int = 64):
+        self.device = device
+        self._caps = (max_seqs, max_rows, max_table_entries, max_query_heads)
+        self._metas = {}
+
+    def name(self) -> str:
+        return "hip-gfx950"
+
+    # mod.rs:73-75
+    def alloc_kv_pool(self, layout: KvLayout) -> KvPool:
+        return KvPool(layout, self.device)
+
+    def kv_layout(self, pool: KvPool) -> KvLayout:
+        out = vo_kv_layout()
+        _check(lib.vo_kv_pool_layout(pool.handle, ctypes.byref(out)))
+        return KvLayout(out.num_layers, out.num_blocks, out.block_size, out.kv_heads,
+                        out.head_dim)
+
+    def step_meta(self, pool: KvPool, slot: str = "step") -> StepMeta:
+        key = (id(pool), slot)
+        m = self._metas.get(key)
+        if m is None:
+            m = StepMeta(pool, *self._caps)
+            self._metas[key] = m
+        return m
+
+    def _meta_for(self, pool: KvPool, meta, stream) -> StepMeta:
+        m = self.step_meta(pool)
+        if m.holds is not meta:
+            m.upload(meta, stream)
+        return m
+
+    # mod.rs:107-119
+    def write_kv(self, pool: KvPool, layer: int, keys, values, slots, stream=None) -> None:
+        """``slots`` is a PrefillMeta/DecodeMeta (its slot mapping) or a slot list."""
+        if isinstance(slots, (PrefillMeta, DecodeMeta)):
+            m = self._meta_for(pool, slots, stream)
+        else:
+            m = self.step_meta(pool, "slots")
+            m.upload_slots(slots, stream)
+        rows = keys.shape[0] if keys.dim() == 2 else 0
+        cols = keys.shape[1] if keys.dim() == 2 else 0
+        if tuple(values.shape) != tuple(keys.shape):
+            raise ValueError("keys and values must have the same shape")
+        _check(lib.vo_write_kv(pool.handle, layer, _dev_ptr(keys), _dev_ptr(values), rows, cols,
+                               m.handle, _stream_ptr(stream)))
+
+    def _attention(self, fn, queries, pool: KvPool, layer: int, meta, out, stream):
+        import torch
+        m = self._meta_for(pool, meta, stream)
+        if out is None:
+            out = torch.empty_like(queries)
+        _check(fn(_dev_ptr(queries), queries.shape[0], queries.shape[1], pool.handle, layer,
+                  m.handle, _dev_ptr(out), _stream_ptr(stream)))
+        return out
+
+    # mod.rs:121-135
+    def prefill_attention(self, queries, pool: KvPool, layer: int, meta: PrefillMeta, out=None,
+                          stream=None):
+        return self._attention(lib.vo_prefill_attention, queries, pool, layer, meta, out, stream)
+
+    # mod.rs:137-149
+    def decode_attention(self, queries, pool: KvPool, layer: int, meta: DecodeMeta, out=None,
+                         stream=None):
+        return self._attention(lib.vo_decode_attention, queries, pool, layer, meta, out, stream)
+
+    def read_kv(self, pool: KvPool, layer: int, meta, seq: int, num_keys: int, stream=None):
+        """Keys and values 0..num_keys of sequence ``seq``, [num_keys, kv_heads*head_dim]."""
+        import torch
+        m = self._meta_for(pool, meta, stream)
+        width = pool.layout.kv_heads * pool.layout.head_dim
+        k = torch.empty((max(num_keys, 1), width), dtype=torch.bfloat16,
+                        device=f"cuda:{self.device}")
+        v = torch.empty_like(k)
+        _check(lib.vo_gather_kv(pool.handle, layer, m.handle, seq, num_keys, _dev_ptr(k),
+                                _dev_ptr(v), _stream_ptr(stream)))
+        return k[:num_keys], v[:num_keys]

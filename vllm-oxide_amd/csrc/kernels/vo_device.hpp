@@ -1,0 +1,60 @@
+// vo_device.hpp -- device-side types and the physical KV-pool layout.
+//
+// Pool layout (backend-private; the reference leaves the bytes to the
+// backend, crates/engine/src/backend/mod.rs:10-12).  Per layer:
+//
+//   K: [num_blocks][kv_heads][block_size][head_dim]   bf16   ("key-major tile")
+//   V: [num_blocks][kv_heads][head_dim][block_size]   bf16   ("dim-major tile")
+//
+// One (block, kv_head) tile is block_size*head_dim*2 bytes contiguous for K
+// and for V (4 KiB at bs 16, hd 128).  K keeps a key's head_dim values
+// together, which is the row operand of the Q.K^T MFMA; V keeps a dim's
+// block_size keys together, which is the row operand of the V^T.P MFMA.
+// The logical slot semantics are the reference's: slot = block*bs + offset
+// (crates/engine/src/backend/paged.rs:25-28).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vo {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Widening bf16 -> f32 is exact: the bf16 bits are the top half of the f32.
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even f32 -> bf16 (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+struct PoolDims {
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t block_size;
+};
+
+// Element offset of K[block][kvh][t][d] within one layer's K region.
+__device__ __forceinline__ uint64_t k_offset(const PoolDims &p, uint32_t block, uint32_t kvh,
+                                             uint32_t t, uint32_t d) {
+    return (static_cast<uint64_t>(block) * p.kv_heads + kvh) * (p.block_size * p.head_dim) +
+           static_cast<uint64_t>(t) * p.head_dim + d;
+}
+
+// Element offset of V[block][kvh][d][t] within one layer's V region.
+__device__ __forceinline__ uint64_t v_offset(const PoolDims &p, uint32_t block, uint32_t kvh,
+                                             uint32_t t, uint32_t d) {
+    return (static_cast<uint64_t>(block) * p.kv_heads + kvh) * (p.block_size * p.head_dim) +
+           static_cast<uint64_t>(d) * p.block_size + t;
+}
+
+}  // namespace vo

@@ -1,0 +1,90 @@
+// vo_kernels.hpp -- host-side launchers of the gfx950 kernels.
+//
+// Callers (vo_backend.cpp) validate every input on the host first; the
+// launchers assume in-bounds metadata and only check launch-shape limits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vo {
+namespace kernels {
+
+// Brackets one kernel launch with HIP events on `stream` when profiling is
+// enabled (vo_profiling_enable); a no-op otherwise.  Declare it in the scope
+// of the launch; the stop event is recorded when it goes out of scope.
+class KernelTimer {
+   public:
+    KernelTimer(const char *name, hipStream_t stream);
+    ~KernelTimer();
+    KernelTimer(const KernelTimer &) = delete;
+    KernelTimer &operator=(const KernelTimer &) = delete;
+
+   private:
+    const char *name_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+};
+
+// One layer of the pool: K and V regions plus the dims that index them.
+struct PoolLayer {
+    uint16_t *k;
+    uint16_t *v;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t block_size;
+};
+
+// Device metadata of one step (all u32, device pointers).
+struct MetaView {
+    const uint32_t *table_off;     // [S+1]
+    const uint32_t *tables;        // [entries]
+    const uint32_t *row_seq;       // [T]
+    const uint32_t *row_num_keys;  // [T]
+    const uint32_t *slot_mapping;  // [T]
+    uint32_t num_rows;
+    uint32_t num_seqs;
+};
+
+// reshape_and_cache: pool[slot_mapping[t]] = keys[t], values[t].
+// keys/values: [rows, kv_heads*head_dim] bf16.  Rows whose slot is
+// kSkipSlot (0xffffffff) are superseded by a later row and not written.
+constexpr uint32_t kSkipSlot = 0xffffffffu;
+hipError_t launch_reshape_and_cache(const PoolLayer &pool, const uint16_t *keys,
+                                    const uint16_t *values, const uint32_t *slot_mapping,
+                                    uint32_t rows, hipStream_t stream);
+
+// Gather keys 0..num_keys of one sequence, whose block table is the device
+// array `table`, into [num_keys, kv_heads*head_dim] (the reference's layout).
+hipError_t launch_gather_kv(const PoolLayer &pool, const uint32_t *table, uint32_t num_keys,
+                            uint16_t *out_k, uint16_t *out_v, hipStream_t stream);
+
+// Generic paged attention for any shape: one workgroup per (row, head),
+// online softmax over 256-key chunks, fp32 accumulation.
+hipError_t launch_attention_generic(const PoolLayer &pool, const MetaView &meta,
+                                    const uint16_t *q, uint16_t *out, uint32_t num_heads,
+                                    float scale, hipStream_t stream);
+
+// Split-K work plan for the MFMA decode kernel.
+struct DecodePlan {
+    const uint32_t *work;         // [num_work][2]: (row, split)
+    const uint32_t *row_part;     // [T]: first partial index of each row
+    uint32_t num_work;
+    uint32_t split_keys;          // keys per split, a multiple of 32
+    float *part_acc;              // [parts][num_heads][head_dim]
+    float *part_ml;               // [parts][num_heads][2]: (max, sum), log2 domain
+    bool needs_reduce;            // some row has zero keys or more than one split
+};
+
+// True when the MFMA decode kernel covers this shape.
+bool decode_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t group);
+
+// MFMA split-K decode (one launch) + reduce (one launch).
+hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
+                              const DecodePlan &plan, const uint16_t *q, uint16_t *out,
+                              uint32_t num_heads, float scale, int waves_per_group,
+                              hipStream_t stream);
+
+}  // namespace kernels
+}  // namespace vo

@@ -1,0 +1,734 @@
+// vo_backend.cpp -- the HIP backend behind the C ABI: KV pool, device-resident
+// step metadata, and the attention-path ops with the reference's checks.
+//
+// Each op validates on the host, in the reference's order, before anything is
+// enqueued (crates/engine/src/arena/ops.rs:102-214, backend/cpu/mod.rs:257-339,
+// backend/cpu/attention.rs:130-147), then launches the kernels on the
+// caller's stream without synchronising.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kernels/vo_kernels.hpp"
+#include "vo_paged.hpp"
+
+using namespace vo;
+
+namespace {
+
+constexpr uint32_t kSkipSlot = 0xffffffffu;  // row superseded by a later row
+constexpr uint64_t kU32Limit = 0x7fffffffull;
+
+// Makes `device` current for the scope and restores the caller's device.
+class DeviceGuard {
+   public:
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != device) ok_ = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+    }
+    bool ok() const { return ok_; }
+
+   private:
+    int prev_ = -1;
+    bool ok_ = true;
+};
+
+uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+
+int env_int(const char *name, int fallback) {
+    const char *v = std::getenv(name);
+    if (!v || !*v) return fallback;
+    return std::atoi(v);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// KV pool
+// ---------------------------------------------------------------------------
+struct vo_kv_pool {
+    vo_kv_layout layout{};
+    int device = 0;
+    int num_cus = 256;
+    uint16_t *base = nullptr;   // [layers][K|V][layer_elems] bf16
+    uint64_t layer_elems = 0;   // elements of one layer's K (or V)
+    uint64_t bytes = 0;
+
+    kernels::PoolLayer layer(uint64_t l) const {
+        kernels::PoolLayer p;
+        p.k = base + l * 2 * layer_elems;
+        p.v = p.k + layer_elems;
+        p.kv_heads = static_cast<uint32_t>(layout.kv_heads);
+        p.head_dim = static_cast<uint32_t>(layout.head_dim);
+        p.block_size = static_cast<uint32_t>(layout.block_size);
+        return p;
+    }
+};
+
+extern "C" int32_t vo_kv_pool_create(const vo_kv_layout *layout, int32_t device,
+                                     vo_kv_pool **out) {
+    if (!layout || !out) return fail_argument("alloc_kv_pool", "null layout or output");
+    *out = nullptr;
+    const vo_kv_layout &L = *layout;
+    if (L.num_layers == 0 || L.num_blocks == 0 || L.block_size == 0 || L.kv_heads == 0 ||
+        L.head_dim == 0)
+        return fail_shape("alloc_kv_pool", "every layout dimension must be non-zero");
+    if (L.head_dim % 8 != 0)
+        return fail_unsupported("alloc_kv_pool",
+                                "head_dim " + std::to_string(L.head_dim) +
+                                    " is not a multiple of 8 (16-byte rows)");
+    if (L.num_blocks * L.block_size > 0xffffffffull)
+        return fail_capacity("kv slots (u32 slot ids)", L.num_blocks * L.block_size,
+                             0xffffffffull);
+    DeviceGuard guard(device);
+    if (!guard.ok()) return fail_device("alloc_kv_pool", hipErrorInvalidDevice, "hipSetDevice");
+    vo_kv_pool *pool = new (std::nothrow) vo_kv_pool();
+    if (!pool) return fail_argument("alloc_kv_pool", "out of host memory");
+    pool->layout = L;
+    pool->device = device;
+    pool->layer_elems = vo_kv_layout_layer_elems(&L);
+    pool->bytes = L.num_layers * 2 * pool->layer_elems * sizeof(uint16_t);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+        pool->num_cus = prop.multiProcessorCount;
+    hipError_t err = hipMalloc(reinterpret_cast<void **>(&pool->base), pool->bytes);
+    if (err != hipSuccess) {
+        delete pool;
+        return fail_device("alloc_kv_pool", err, hipGetErrorString(err));
+    }
+    // Zero-filled, as the reference's calloc'd pool (cpu/mod.rs:148-157).
+    err = hipMemset(pool->base, 0, pool->bytes);
+    if (err != hipSuccess) {
+        (void)hipFree(pool->base);
+        delete pool;
+        return fail_device("alloc_kv_pool", err, hipGetErrorString(err));
+    }
+    *out = pool;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" void vo_kv_pool_destroy(vo_kv_pool *pool) {
+    if (!pool) return;
+    DeviceGuard guard(pool->device);
+    (void)hipFree(pool->base);
+    delete pool;
+}
+
+extern "C" int32_t vo_kv_pool_layout(const vo_kv_pool *pool, vo_kv_layout *out) {
+    if (!pool || !out) return fail_argument("kv_layout", "null pool or output");
+    *out = pool->layout;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" uint64_t vo_kv_pool_bytes(const vo_kv_pool *pool) { return pool ? pool->bytes : 0; }
+
+// ---------------------------------------------------------------------------
+// Step metadata
+// ---------------------------------------------------------------------------
+namespace {
+enum MetaKind { kNone = 0, kPrefill = 1, kDecode = 2, kSlots = 3 };
+}
+
+struct vo_step_meta {
+    int device = 0;
+    int num_cus = 256;
+    uint64_t pool_block_size = 0;
+    uint64_t kv_heads = 0;
+    uint64_t head_dim = 0;
+
+    uint64_t max_seqs = 0, max_rows = 0, max_entries = 0, max_heads = 0, max_parts = 0;
+
+    MetaKind kind = kNone;
+    uint64_t block_size = 0;
+    uint64_t num_seqs = 0;
+    uint64_t num_rows = 0;
+
+    // Host copies, for validation with the reference's error semantics.
+    std::vector<uint64_t> table_off;    // [S+1]
+    std::vector<uint32_t> tables;       // [entries]
+    std::vector<uint32_t> slots;        // [T] as given
+    std::vector<uint32_t> row_seq;      // [T]
+    std::vector<uint32_t> row_num_keys; // [T]
+    uint32_t max_block = 0;             // max table entry (0 if none)
+    uint32_t max_slot = 0;              // max slot (0 if none)
+
+    // Device buffer and pinned staging of the same size.
+    uint8_t *d_buf = nullptr;
+    uint8_t *h_stage = nullptr;
+    uint64_t buf_bytes = 0;
+    hipEvent_t copy_done = nullptr;
+    bool copy_pending = false;
+
+    // Split-K partials (fp32).
+    float *d_part_acc = nullptr;
+    float *d_part_ml = nullptr;
+
+    kernels::MetaView view{};
+    const uint32_t *d_write_slots = nullptr;  // slots with superseded rows = kSkipSlot
+    kernels::DecodePlan plan{};
+    bool decode_planned = false;
+};
+
+namespace {
+
+// Packs u32 arrays back to back (256-byte aligned) into the staging buffer and
+// records each array's device address.  The buffer is sized at creation for
+// the declared capacities; should a request still not fit, the arrays go to a
+// host-side sink and fits() reports it, so nothing is written out of bounds.
+class Packer {
+   public:
+    explicit Packer(vo_step_meta *m) : m_(m) {}
+    uint32_t *add(uint64_t count, const uint32_t **device_ptr) {
+        off_ = align_up(off_, 256);
+        const uint64_t end = off_ + count * sizeof(uint32_t);
+        if (end > m_->buf_bytes || overflow_) {
+            overflow_ = true;
+            off_ = end;
+            sinks_.emplace_back(count + 1);
+            *device_ptr = nullptr;
+            return sinks_.back().data();
+        }
+        uint32_t *host = reinterpret_cast<uint32_t *>(m_->h_stage + off_);
+        *device_ptr = reinterpret_cast<const uint32_t *>(m_->d_buf + off_);
+        off_ = end;
+        return host;
+    }
+    uint64_t used() const { return off_; }
+    bool fits() const { return !overflow_; }
+
+   private:
+    vo_step_meta *m_;
+    uint64_t off_ = 0;
+    bool overflow_ = false;
+    std::vector<std::vector<uint32_t>> sinks_;
+};
+
+vo_status wait_previous_copy(vo_step_meta *m, const char *op) {
+    if (m->copy_pending) {
+        hipError_t err = hipEventSynchronize(m->copy_done);
+        if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
+        m->copy_pending = false;
+    }
+    return VO_OK;
+}
+
+vo_status finish_upload(vo_step_meta *m, const Packer &pk, hipStream_t stream, const char *op) {
+    if (pk.used() > 0) {
+        hipError_t err = hipMemcpyAsync(m->d_buf, m->h_stage, pk.used(), hipMemcpyHostToDevice,
+                                        stream);
+        if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
+        err = hipEventRecord(m->copy_done, stream);
+        if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
+        m->copy_pending = true;
+    }
+    return VO_OK;
+}
+
+// CSR block tables: offsets start at 0 and never decrease.
+vo_status check_tables(const char *op, uint64_t num_seqs, const uint64_t *table_off,
+                       const uint32_t *tables, uint64_t max_entries) {
+    if (!table_off) return fail_argument(op, "null table offsets");
+    if (table_off[0] != 0) return fail_shape(op, "table offsets must start at 0");
+    for (uint64_t s = 0; s < num_seqs; ++s)
+        if (table_off[s + 1] < table_off[s])
+            return fail_shape(op, "table offsets decrease at sequence " + std::to_string(s));
+    const uint64_t entries = table_off[num_seqs];
+    if (entries > max_entries) return fail_capacity("block-table entries per step", entries, max_entries);
+    if (entries && !tables) return fail_argument(op, "null block tables");
+    return VO_OK;
+}
+
+// Rows: sequence index in range; key count covered by the sequence's table
+// (what PrefillMeta::new / DecodeMeta::new guarantee, paged.rs:130, :200).
+vo_status check_rows(const char *op, uint64_t num_rows, uint64_t num_seqs, uint64_t block_size,
+                     const uint64_t *table_off, const uint64_t *row_seq,
+                     const uint64_t *row_num_keys) {
+    if (num_rows && (!row_seq || !row_num_keys)) return fail_argument(op, "null row arrays");
+    for (uint64_t r = 0; r < num_rows; ++r) {
+        if (row_seq[r] >= num_seqs)
+            return fail_shape(op, "row " + std::to_string(r) + " names sequence " +
+                                      std::to_string(row_seq[r]) + " of " +
+                                      std::to_string(num_seqs));
+        if (row_num_keys[r] > kU32Limit)
+            return fail_capacity("keys per row", row_num_keys[r], kU32Limit);
+        const uint64_t s = row_seq[r];
+        if (vo_status rc = check_covers(op, table_off[s + 1] - table_off[s], row_num_keys[r],
+                                        block_size, s))
+            return rc;
+    }
+    return VO_OK;
+}
+
+// Common part of the prefill and decode uploads.
+vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t block_size,
+                        uint64_t num_seqs, const uint64_t *table_off, const uint32_t *tables,
+                        uint64_t num_rows, const uint32_t *slot_mapping, const uint64_t *row_seq,
+                        const uint64_t *row_num_keys, Packer &pk) {
+    if (block_size == 0) return fail_shape(op, "block_size 0");
+    if (num_seqs > m->max_seqs) return fail_capacity("sequences per step", num_seqs, m->max_seqs);
+    if (num_rows > m->max_rows) return fail_capacity("tokens per step", num_rows, m->max_rows);
+    if (vo_status rc = check_tables(op, num_seqs, table_off, tables, m->max_entries)) return rc;
+    if (kind != kSlots) {
+        if (vo_status rc =
+                check_rows(op, num_rows, num_seqs, block_size, table_off, row_seq, row_num_keys))
+            return rc;
+    }
+    if (num_rows && !slot_mapping) return fail_argument(op, "null slot mapping");
+    if (vo_status rc = wait_previous_copy(m, op)) return rc;
+
+    const uint64_t entries = table_off[num_seqs];
+    m->kind = kind;
+    m->block_size = block_size;
+    m->num_seqs = num_seqs;
+    m->num_rows = num_rows;
+    m->table_off.assign(table_off, table_off + num_seqs + 1);
+    m->tables.assign(tables, tables + entries);
+    m->slots.assign(slot_mapping, slot_mapping + num_rows);
+    m->row_seq.resize(num_rows);
+    m->row_num_keys.resize(num_rows);
+    m->max_block = 0;
+    for (uint32_t b : m->tables) m->max_block = std::max(m->max_block, b);
+    m->max_slot = 0;
+    for (uint32_t s : m->slots) m->max_slot = std::max(m->max_slot, s);
+
+    const uint32_t *dp;
+    uint32_t *h = pk.add(num_seqs + 1, &dp);
+    for (uint64_t s = 0; s <= num_seqs; ++s) h[s] = static_cast<uint32_t>(table_off[s]);
+    m->view.table_off = dp;
+    h = pk.add(entries, &dp);
+    if (entries) std::memcpy(h, tables, entries * sizeof(uint32_t));
+    m->view.tables = dp;
+    h = pk.add(num_rows, &dp);
+    for (uint64_t r = 0; r < num_rows; ++r)
+        h[r] = m->row_seq[r] = row_seq ? static_cast<uint32_t>(row_seq[r]) : 0u;
+    m->view.row_seq = dp;
+    h = pk.add(num_rows, &dp);
+    for (uint64_t r = 0; r < num_rows; ++r)
+        h[r] = m->row_num_keys[r] = row_num_keys ? static_cast<uint32_t>(row_num_keys[r]) : 0u;
+    m->view.row_num_keys = dp;
+    // Write slots: a slot that appears again later keeps only its last row,
+    // the reference's "later row wins" copy order (cpu/mod.rs:277-283).
+    h = pk.add(num_rows, &dp);
+    {
+        std::unordered_map<uint32_t, uint64_t> last;
+        bool dup = false;
+        last.reserve(num_rows * 2);
+        for (uint64_t r = 0; r < num_rows; ++r) {
+            auto it = last.find(slot_mapping[r]);
+            if (it != last.end()) dup = true;
+            last[slot_mapping[r]] = r;
+        }
+        for (uint64_t r = 0; r < num_rows; ++r)
+            h[r] = (!dup || last[slot_mapping[r]] == r) ? slot_mapping[r] : kSkipSlot;
+    }
+    m->d_write_slots = dp;
+    m->view.slot_mapping = dp;
+    m->view.num_rows = static_cast<uint32_t>(num_rows);
+    m->view.num_seqs = static_cast<uint32_t>(num_seqs);
+    m->decode_planned = false;
+    return VO_OK;
+}
+
+// Split-K plan.  Every row's keys are cut into splits of L keys (a multiple
+// of 32, default kDefaultSplit).  L does not depend on the rest of the batch,
+// so a row's arithmetic -- which keys each wavefront accumulates, in which
+// order, and how the partials merge -- is the same alone or in any batch:
+// the reference's batch-invariance invariant (CLAUDE.md "Batch invariance",
+// model.rs:539-584).  VO_DECODE_SPLIT overrides L (a tuning knob).
+constexpr uint64_t kDefaultSplit = 512;
+
+uint64_t decode_split_keys() {
+    const int env = env_int("VO_DECODE_SPLIT", 0);
+    return (env >= 32 && env % 32 == 0) ? static_cast<uint64_t>(env) : kDefaultSplit;
+}
+
+vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
+    const uint64_t T = m->num_rows;
+    const uint64_t L = decode_split_keys();
+    uint64_t parts = 0;
+    for (uint64_t r = 0; r < T; ++r) parts += (m->row_num_keys[r] + L - 1) / L;
+    if (parts > m->max_parts) return fail_capacity("split-K partials per step", parts, m->max_parts);
+    (void)op;
+
+    const uint32_t *dp;
+    uint32_t *work = pk.add(2 * parts, &dp);
+    m->plan.work = dp;
+    uint32_t *row_part = pk.add(T, &dp);
+    m->plan.row_part = dp;
+    uint64_t n = 0;
+    bool needs_reduce = false;
+    for (uint64_t r = 0; r < T; ++r) {
+        const uint64_t ns = (m->row_num_keys[r] + L - 1) / L;
+        row_part[r] = static_cast<uint32_t>(n);
+        if (ns != 1) needs_reduce = true;
+        for (uint64_t s = 0; s < ns; ++s, ++n) {
+            work[2 * n] = static_cast<uint32_t>(r);
+            work[2 * n + 1] = static_cast<uint32_t>(s);
+        }
+    }
+    m->plan.num_work = static_cast<uint32_t>(parts);
+    m->plan.split_keys = static_cast<uint32_t>(L);
+    m->plan.part_acc = m->d_part_acc;
+    m->plan.part_ml = m->d_part_ml;
+    m->plan.needs_reduce = needs_reduce;
+    m->decode_planned = true;
+    return VO_OK;
+}
+
+int decode_waves() {
+    int w = env_int("VO_DECODE_WAVES", 4);
+    return (w == 1 || w == 2 || w == 4) ? w : 4;
+}
+
+}  // namespace
+
+extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs,
+                                       uint64_t max_rows, uint64_t max_table_entries,
+                                       uint64_t max_query_heads, vo_step_meta **out) {
+    const char *op = "step_meta_create";
+    if (!pool || !out) return fail_argument(op, "null pool or output");
+    *out = nullptr;
+    if (max_seqs == 0 || max_rows == 0 || max_query_heads == 0)
+        return fail_argument(op, "capacities must be non-zero");
+    if (max_seqs > kU32Limit || max_rows > kU32Limit || max_table_entries > kU32Limit)
+        return fail_capacity("step metadata entries (u32)", std::max({max_seqs, max_rows, max_table_entries}),
+                             kU32Limit);
+    DeviceGuard guard(pool->device);
+    if (!guard.ok()) return fail_device(op, hipErrorInvalidDevice, "hipSetDevice");
+    vo_step_meta *m = new (std::nothrow) vo_step_meta();
+    if (!m) return fail_argument(op, "out of host memory");
+    m->device = pool->device;
+    m->num_cus = pool->num_cus;
+    m->pool_block_size = pool->layout.block_size;
+    m->kv_heads = pool->layout.kv_heads;
+    m->head_dim = pool->layout.head_dim;
+    m->max_seqs = max_seqs;
+    m->max_rows = max_rows;
+    m->max_entries = max_table_entries;
+    m->max_heads = max_query_heads;
+    // Decode partials: one per (row, split).  With one row per sequence the
+    // keys of a step are at most entries * block_size, so rows + keys / L
+    // bounds the splits (L as configured when the meta is created).
+    m->max_parts = max_rows + (max_table_entries * pool->layout.block_size) / decode_split_keys();
+
+    const uint64_t u32s = (max_seqs + 1) + max_table_entries + 3 * max_rows  // offsets, tables, row arrays
+                          + max_rows                                         // write slots
+                          + 2 * m->max_parts + max_rows                      // decode plan
+                          + 8 * 64;                                          // alignment slack
+    m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
+    hipError_t err = hipMalloc(reinterpret_cast<void **>(&m->d_buf), m->buf_bytes);
+    if (err == hipSuccess)
+        err = hipHostMalloc(reinterpret_cast<void **>(&m->h_stage), m->buf_bytes, hipHostMallocDefault);
+    if (err == hipSuccess)
+        err = hipMalloc(reinterpret_cast<void **>(&m->d_part_acc),
+                        m->max_parts * max_query_heads * m->head_dim * sizeof(float));
+    if (err == hipSuccess)
+        err = hipMalloc(reinterpret_cast<void **>(&m->d_part_ml),
+                        m->max_parts * max_query_heads * 2 * sizeof(float));
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&m->copy_done, hipEventDisableTiming);
+    if (err != hipSuccess) {
+        vo_status rc = fail_device(op, err, hipGetErrorString(err));
+        if (m->d_buf) (void)hipFree(m->d_buf);
+        if (m->h_stage) (void)hipHostFree(m->h_stage);
+        if (m->d_part_acc) (void)hipFree(m->d_part_acc);
+        if (m->d_part_ml) (void)hipFree(m->d_part_ml);
+        delete m;
+        return rc;
+    }
+    *out = m;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" void vo_step_meta_destroy(vo_step_meta *m) {
+    if (!m) return;
+    DeviceGuard guard(m->device);
+    if (m->copy_pending) (void)hipEventSynchronize(m->copy_done);
+    if (m->copy_done) (void)hipEventDestroy(m->copy_done);
+    (void)hipFree(m->d_buf);
+    (void)hipHostFree(m->h_stage);
+    (void)hipFree(m->d_part_acc);
+    (void)hipFree(m->d_part_ml);
+    delete m;
+}
+
+extern "C" int32_t vo_step_meta_upload_prefill(
+    vo_step_meta *m, uint64_t block_size, uint64_t num_seqs, const uint64_t *table_off,
+    const uint32_t *tables, const uint64_t *context_lens, const uint64_t *seq_row_starts,
+    uint64_t num_rows, const uint32_t *positions, const uint32_t *slot_mapping,
+    const uint64_t *row_seq, const uint64_t *row_num_keys, void *stream) {
+    const char *op = "prefill";
+    if (!m) return fail_argument(op, "null meta");
+    (void)positions;  // positions feed RoPE, which runs before the cache write
+    if (num_seqs && (!context_lens || !seq_row_starts))
+        return fail_argument(op, "null context_lens or seq_row_starts");
+    if (seq_row_starts && (seq_row_starts[0] != 0 || seq_row_starts[num_seqs] != num_rows))
+        return fail_shape(op, "seq_row_starts must run from 0 to num_rows");
+    for (uint64_t s = 0; s < num_seqs; ++s)
+        if (seq_row_starts[s + 1] < seq_row_starts[s])
+            return fail_shape(op, "seq_row_starts decrease at sequence " + std::to_string(s));
+    DeviceGuard guard(m->device);
+    Packer pk(m);
+    if (vo_status rc = upload_common(m, kPrefill, op, block_size, num_seqs, table_off, tables,
+                                     num_rows, slot_mapping, row_seq, row_num_keys, pk))
+        return rc;
+    if (!pk.fits()) {
+        m->kind = kNone;
+        return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
+    }
+    if (vo_status rc = finish_upload(m, pk, static_cast<hipStream_t>(stream), op)) return rc;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" int32_t vo_step_meta_upload_decode(vo_step_meta *m, uint64_t block_size,
+                                              uint64_t num_seqs, const uint64_t *table_off,
+                                              const uint32_t *tables, const uint32_t *positions,
+                                              const uint32_t *slot_mapping,
+                                              const uint64_t *row_seq,
+                                              const uint64_t *row_num_keys, void *stream) {
+    const char *op = "decode";
+    if (!m) return fail_argument(op, "null meta");
+    (void)positions;
+    DeviceGuard guard(m->device);
+    Packer pk(m);
+    if (vo_status rc = upload_common(m, kDecode, op, block_size, num_seqs, table_off, tables,
+                                     num_seqs, slot_mapping, row_seq, row_num_keys, pk))
+        return rc;
+    if (vo_status rc = plan_decode(m, pk, op)) {
+        m->kind = kNone;
+        return rc;
+    }
+    if (!pk.fits()) {
+        m->kind = kNone;
+        return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
+    }
+    if (vo_status rc = finish_upload(m, pk, static_cast<hipStream_t>(stream), op)) return rc;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" int32_t vo_step_meta_upload_slots(vo_step_meta *m, const uint32_t *slots,
+                                             uint64_t num_slots, void *stream) {
+    const char *op = "write_kv";
+    if (!m) return fail_argument(op, "null meta");
+    DeviceGuard guard(m->device);
+    const uint64_t zero = 0;
+    Packer pk(m);
+    if (vo_status rc = upload_common(m, kSlots, op, m->pool_block_size ? m->pool_block_size : 1, 0,
+                                     &zero, nullptr, num_slots, slots, nullptr, nullptr, pk))
+        return rc;
+    if (!pk.fits()) {
+        m->kind = kNone;
+        return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
+    }
+    if (vo_status rc = finish_upload(m, pk, static_cast<hipStream_t>(stream), op)) return rc;
+    clear_error();
+    return VO_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Ops
+// ---------------------------------------------------------------------------
+namespace {
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool overlaps(const void *a, uint64_t a_bytes, const void *b, uint64_t b_bytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a_bytes && b_bytes && a0 < b0 + b_bytes && b0 < a0 + a_bytes;
+}
+
+std::string layout_text(const vo_kv_layout &L) {
+    return "KvLayout { num_layers: " + std::to_string(L.num_layers) +
+           ", num_blocks: " + std::to_string(L.num_blocks) +
+           ", block_size: " + std::to_string(L.block_size) +
+           ", kv_heads: " + std::to_string(L.kv_heads) +
+           ", head_dim: " + std::to_string(L.head_dim) + " }";
+}
+
+// arena/ops.rs:191-214 (check_attention) plus the pointer checks a C ABI needs.
+vo_status check_attention(const char *op, const void *queries, uint64_t rows, uint64_t cols,
+                          const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *m,
+                          const void *out, MetaKind want) {
+    if (!pool || !m) return fail_argument(op, "null pool or meta");
+    const vo_kv_layout &L = pool->layout;
+    const bool shape_ok = rows == m->num_rows && cols % L.head_dim == 0 &&
+                          (cols / L.head_dim) % L.kv_heads == 0 && layer < L.num_layers &&
+                          m->block_size == L.block_size;
+    if (!shape_ok || m->kind != want) {
+        std::string msg = "queries [" + std::to_string(rows) + ", " + std::to_string(cols) + "], " +
+                          std::to_string(m->num_rows) + " rows in metadata, block size " +
+                          std::to_string(m->block_size) + ", layer " + std::to_string(layer) +
+                          ", pool " + layout_text(L);
+        if (m->kind != want)
+            msg += want == kPrefill ? "; metadata is not a prefill upload"
+                                    : "; metadata is not a decode upload";
+        return fail_shape(op, msg);
+    }
+    if (rows == 0) return VO_OK;
+    if (!queries || !out) return fail_argument(op, "null queries or output");
+    if (!aligned16(queries) || !aligned16(out))
+        return fail_argument(op, "queries and output must be 16-byte aligned");
+    const uint64_t bytes = rows * cols * sizeof(uint16_t);
+    if (overlaps(queries, bytes, out, bytes)) return fail_shape(op, "output overlaps queries");
+    const uint64_t heads = cols / L.head_dim;
+    if (heads > m->max_heads) return fail_capacity("query heads", heads, m->max_heads);
+    if (heads > 0xffffull) return fail_capacity("query heads", heads, 0xffff);
+    // attention.rs:130-147, against this pool's block count.
+    if (m->max_block >= L.num_blocks)
+        return check_block_tables(op, m->num_seqs, m->table_off.data(), m->tables.data(),
+                                  L.num_blocks);
+    return VO_OK;
+}
+
+vo_status device_status(const char *op, hipError_t err) {
+    if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
+    clear_error();
+    return VO_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys,
+                               const void *values, uint64_t rows, uint64_t cols,
+                               const vo_step_meta *m, void *stream) {
+    const char *op = "write_kv";
+    if (!pool || !m) return fail_argument(op, "null pool or meta");
+    const vo_kv_layout &L = pool->layout;
+    const uint64_t slot_width = L.kv_heads * L.head_dim;
+    // arena/ops.rs:116-127
+    const bool shape_ok = rows == m->num_rows && cols == slot_width && layer < L.num_layers;
+    if (!shape_ok || m->kind == kNone)
+        return fail_shape(op, "keys [" + std::to_string(rows) + ", " + std::to_string(cols) +
+                                  "], values [" + std::to_string(rows) + ", " +
+                                  std::to_string(cols) + "], " + std::to_string(m->num_rows) +
+                                  " slots, layer " + std::to_string(layer) + ", pool " +
+                                  layout_text(L));
+    // cpu/mod.rs:265-272: every slot in range before any write.
+    const uint64_t num_slots = vo_kv_layout_num_slots(&L);
+    if (rows && m->max_slot >= num_slots) {
+        for (uint32_t s : m->slots) {
+            if (s >= num_slots) {
+                Error e;
+                e.status = VO_ERR_SLOT_OUT_OF_RANGE;
+                e.op = op;
+                e.value = s;
+                e.limit = num_slots;
+                e.message = std::string(op) + ": slot " + std::to_string(s) +
+                            " out of range (pool has " + std::to_string(num_slots) + ")";
+                return fail(e);
+            }
+        }
+    }
+    if (rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!keys || !values) return fail_argument(op, "null keys or values");
+    if (!aligned16(keys) || !aligned16(values))
+        return fail_argument(op, "keys and values must be 16-byte aligned");
+    DeviceGuard guard(pool->device);
+    hipError_t err = kernels::launch_reshape_and_cache(
+        pool->layer(layer), static_cast<const uint16_t *>(keys),
+        static_cast<const uint16_t *>(values), m->d_write_slots, static_cast<uint32_t>(rows),
+        static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_prefill_attention(const void *queries, uint64_t rows, uint64_t cols,
+                                        const vo_kv_pool *pool, uint64_t layer,
+                                        const vo_step_meta *m, void *out, void *stream) {
+    const char *op = "prefill_attention";
+    if (vo_status rc = check_attention(op, queries, rows, cols, pool, layer, m, out, kPrefill))
+        return rc;
+    if (rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    const vo_kv_layout &L = pool->layout;
+    const uint32_t heads = static_cast<uint32_t>(cols / L.head_dim);
+    const float scale = 1.0f / std::sqrt(static_cast<float>(L.head_dim));  // attention.rs:88
+    DeviceGuard guard(pool->device);
+    hipError_t err = kernels::launch_attention_generic(
+        pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),
+        static_cast<uint16_t *>(out), heads, scale, static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_decode_attention(const void *queries, uint64_t rows, uint64_t cols,
+                                       const vo_kv_pool *pool, uint64_t layer,
+                                       const vo_step_meta *m, void *out, void *stream) {
+    const char *op = "decode_attention";
+    if (vo_status rc = check_attention(op, queries, rows, cols, pool, layer, m, out, kDecode))
+        return rc;
+    if (rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    const vo_kv_layout &L = pool->layout;
+    const uint32_t heads = static_cast<uint32_t>(cols / L.head_dim);
+    const uint32_t group = heads / static_cast<uint32_t>(L.kv_heads);
+    const float scale = 1.0f / std::sqrt(static_cast<float>(L.head_dim));  // attention.rs:88
+    DeviceGuard guard(pool->device);
+    hipError_t err;
+    if (kernels::decode_mfma_supported(static_cast<uint32_t>(L.head_dim),
+                                       static_cast<uint32_t>(L.block_size), group) &&
+        m->decode_planned) {
+        err = kernels::launch_decode_mfma(pool->layer(layer), m->view, m->plan,
+                                          static_cast<const uint16_t *>(queries),
+                                          static_cast<uint16_t *>(out), heads, scale,
+                                          decode_waves(), static_cast<hipStream_t>(stream));
+    } else {
+        err = kernels::launch_attention_generic(
+            pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),
+            static_cast<uint16_t *>(out), heads, scale, static_cast<hipStream_t>(stream));
+    }
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_gather_kv(const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *m,
+                                uint64_t seq, uint64_t num_keys, void *out_keys,
+                                void *out_values, void *stream) {
+    const char *op = "read";
+    if (!pool || !m) return fail_argument(op, "null pool or meta");
+    const vo_kv_layout &L = pool->layout;
+    if (layer >= L.num_layers || seq >= m->num_seqs || m->block_size != L.block_size ||
+        (m->kind != kPrefill && m->kind != kDecode))
+        return fail_shape(op, "layer " + std::to_string(layer) + ", sequence " +
+                                  std::to_string(seq) + " of " + std::to_string(m->num_seqs) +
+                                  ", pool " + layout_text(L));
+    const uint64_t t0 = m->table_off[seq], t1 = m->table_off[seq + 1];
+    if (vo_status rc = check_covers(op, t1 - t0, num_keys, L.block_size, seq)) return rc;
+    const uint64_t one_off[2] = {0, t1 - t0};
+    if (vo_status rc = check_block_tables(op, 1, one_off, m->tables.data() + t0, L.num_blocks))
+        return rc;
+    if (num_keys > kU32Limit) return fail_capacity("keys", num_keys, kU32Limit);
+    if (num_keys == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!out_keys || !out_values) return fail_argument(op, "null outputs");
+    if (!aligned16(out_keys) || !aligned16(out_values))
+        return fail_argument(op, "outputs must be 16-byte aligned");
+    DeviceGuard guard(pool->device);
+    hipError_t err = kernels::launch_gather_kv(pool->layer(layer), m->view.tables + t0,
+                                               static_cast<uint32_t>(num_keys),
+                                               static_cast<uint16_t *>(out_keys),
+                                               static_cast<uint16_t *>(out_values),
+                                               static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
