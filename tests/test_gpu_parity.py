@@ -170,13 +170,26 @@ def test_decode_mfma_edge_lengths(vo, gpu_backend, hd, heads, kvh):
     _assert_close(out.float().cpu().numpy(), want, f"decode hd={hd} H={heads} KVH={kvh}")
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_decode_mfma_many_short_rows(vo, gpu_backend, hd):
+    """Rows with 1..48 keys put the softmax weight on few keys, where rounding
+    P to bf16 alone would break the tolerance; 256 rows per head_dim."""
+    _say(f"decode short rows hd={hd}")
+    ctx = np.random.default_rng(hd).integers(0, 48, 256)
+    wl = W.build(vo, gpu_backend, kind="decode", heads=32, kv_heads=8, head_dim=hd,
+                 block_size=16, num_blocks=1200, context_lens=ctx, seed=hd + 1)
+    out = _out(wl, gpu_backend)
+    want = W.oracle_attention(orc, wl)
+    _assert_close(out.float().cpu().numpy(), want, f"short rows hd={hd}")
+
+
 @pytest.mark.parametrize("split,waves", [("32", "1"), ("64", "2"), ("96", "4"), ("512", "1"),
                                          ("512", "2"), ("2048", "4")])
 def test_decode_mfma_split_and_wave_variants(vo, monkeypatch, split, waves):
     monkeypatch.setenv("VO_DECODE_SPLIT", split)
     monkeypatch.setenv("VO_DECODE_WAVES", waves)
     _say(f"decode split={split} waves={waves}")
-    backend = vo.HipBackend(device=0, max_seqs=64, max_rows=64, max_table_entries=4096,
+    backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=4096,
                             max_query_heads=32)
     wl = W.build(vo, backend, kind="decode", heads=32, kv_heads=8, head_dim=128, block_size=16,
                  num_blocks=1500, context_lens=EDGE_CTX, seed=int(split) + int(waves))
@@ -273,9 +286,8 @@ def test_prefill_cfg3_full_size_sampled_rows(vo, gpu_backend):
     wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
                  block_size=16, num_blocks=12000, context_lens=ctx, num_new=[512] * 8, seed=3)
     out = _out(wl, gpu_backend).float().cpu().numpy()
-    rows = np.unique(np.concatenate([np.arange(0, wl.rows, 29),
-                                     np.asarray(wl.meta.seq_row_starts[1:]) - 1,
-                                     np.asarray(wl.meta.seq_row_starts[:-1])]))
+    starts = np.asarray(wl.meta.seq_row_starts, dtype=np.int64)
+    rows = np.unique(np.concatenate([np.arange(0, wl.rows, 29), starts[1:] - 1, starts[:-1]]))
     want = W.oracle_attention(orc, wl, rows=rows)
     _assert_close(out[rows], want, "cfg3")
 

@@ -119,12 +119,34 @@ SIGNATURES = {
 }
 
 
+def _hip_runtimes_mapped() -> List[str]:
+    try:
+        maps = pathlib.Path("/proc/self/maps").read_text()
+    except OSError:
+        return []
+    return sorted({line.split()[-1] for line in maps.splitlines()
+                   if "libamdhip64.so" in line and "/" in line})
+
+
 def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
             f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
             f"g.build()'` (make -C vllm-oxide_amd/csrc).  There is no fallback path.")
+    # PyTorch-ROCm wheels carry their own HIP runtime (SONAME libamdhip64.so.7).
+    # Loading torch first makes the loader bind this library to that same
+    # runtime, so torch's device pointers and streams are valid here.  Loaded
+    # the other way round, two HIP runtimes would coexist in the process.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     handle = ctypes.CDLL(str(LIB_PATH))
+    runtimes = _hip_runtimes_mapped()
+    if len(runtimes) > 1:
+        raise ImportError(
+            "two HIP runtimes are loaded in this process (" + ", ".join(runtimes) + "); "
+            "import torch before anything that loads /opt/rocm's libamdhip64")
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype = res

@@ -31,11 +31,12 @@
 //   P.V:   O^T[d, h] += V^T[d, key] . P^T[key, h] with 16x16x32 MFMAs:
 //          A = 16 dims x 32 keys of V -- lane l reads the 8 keys 8*(l/16)..+7
 //          of dim l%16, which are 16 contiguous bytes of the dim-major V tile
-//          -- and B = P^T, which is exactly the lane's own 8 probabilities in
-//          bf16.  Output rows are dims, columns heads, so the softmax rescale
-//          of the accumulator is lane-local.
+//          -- and B = P^T, which is exactly the lane's own 8 probabilities,
+//          split into bf16 hi and lo parts (two MFMAs) so P keeps ~16 bits.
+//          Output rows are dims, columns heads, so the softmax rescale of the
+//          accumulator is lane-local.
 // Per chunk and KV head a wavefront moves 16 KiB (hd 128) through 16 global
-// loads of 16 bytes per lane and issues 16 MFMAs.
+// loads of 16 bytes per lane and issues 24 MFMAs.
 //
 // Roofline: HBM.  Algorithmic bytes per row = keys * kv_heads * head_dim * 2 B
 // * 2 (K and V) + q and out rows + block-table entries.  The MFMA work is
@@ -168,13 +169,19 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
         const float m_new = fmaxf(m_run, mt);  // finite: the chunk has a valid key
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        // P goes to the MFMA as two bf16 parts, hi = bf16(p) and lo = bf16(p - hi),
+        // so the probabilities keep ~16 significant bits instead of bf16's 8;
+        // bf16 P alone exceeds rtol 1e-2 / atol 2e-3 on rows whose weight sits
+        // on a few keys.
         float ps = 0.0f;
-        bf16x8 pb;
+        bf16x8 pb_hi, pb_lo;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float p = __builtin_amdgcn_exp2f(sc[i] - m_new);
             ps += p;
-            pb[i] = static_cast<__bf16>(p);
+            const __bf16 hi = static_cast<__bf16>(p);
+            pb_hi[i] = hi;
+            pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
         }
         l_run = l_run * alpha + ps;
         m_run = m_new;
@@ -191,7 +198,10 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
                     if (jg + i >= k_end) va[dt][i] = static_cast<__bf16>(0.0f);
         }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma16x16x32(va[dt], pb, acc[dt]);
+        for (int dt = 0; dt < DT; ++dt) {
+            acc[dt] = mfma16x16x32(va[dt], pb_lo, acc[dt]);
+            acc[dt] = mfma16x16x32(va[dt], pb_hi, acc[dt]);
+        }
     }
 
     // The running sums are per lane group; the max is already per head.
