@@ -187,7 +187,7 @@ def cpu_baseline(orc, W, wl, nbytes, args):
         t0 = time.perf_counter()
         W.oracle_attention(orc, wl, pool=pool, threads=threads)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() >= t_end or len(times) >= 50:
+        if time.perf_counter() >= t_end or len(times) >= 2000:
             break
     med = float(np.median(times))
     S = wl.rows
@@ -253,6 +253,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (scales the HBM byte "
+                         "counters of rocprofv3 --pmc)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -265,6 +268,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.calibrate_copy:
+        n = 1 << 30
+        src = torch.ones(n // 2, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": n, "bytes_written": n, "launches": 5}))
+        return
+
     vo = _load_package()
     import oracle as orc
     import workloads as W

@@ -184,8 +184,11 @@ def test_decode_mfma_many_short_rows(vo, gpu_backend, hd):
 
 
 @pytest.mark.parametrize("split,waves", [("32", "1"), ("64", "2"), ("96", "4"), ("512", "1"),
-                                         ("512", "2"), ("2048", "4")])
+                                         ("512", "2"), ("2048", "4"), ("4096", "4"), ("32", "4"),
+                                         ("768", "8"), ("4096", "8")])
 def test_decode_mfma_split_and_wave_variants(vo, monkeypatch, split, waves):
+    """Every split size and wavefront count gives the same results within
+    tolerance, and a repeated call is bitwise identical."""
     monkeypatch.setenv("VO_DECODE_SPLIT", split)
     monkeypatch.setenv("VO_DECODE_WAVES", waves)
     _say(f"decode split={split} waves={waves}")
@@ -196,6 +199,8 @@ def test_decode_mfma_split_and_wave_variants(vo, monkeypatch, split, waves):
     out = _out(wl, backend)
     want = W.oracle_attention(orc, wl)
     _assert_close(out.float().cpu().numpy(), want, f"decode split={split} waves={waves}")
+    again = _out(wl, backend)
+    assert np.array_equal(_bits(again), _bits(out))
 
 
 def test_decode_cfg2_full_size(vo, gpu_backend):

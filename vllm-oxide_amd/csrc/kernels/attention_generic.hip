@@ -82,9 +82,10 @@ __global__ __launch_bounds__(kThreads) void attention_generic_kernel(
             const uint32_t block = table[j / dims.block_size];
             const uint32_t t = j % dims.block_size;
             slot = block * dims.block_size + t;
-            const uint16_t *kp = k_pool + k_offset(dims, block, kvh, t, 0);
+            const uint16_t *kp = k_pool + k_offset(dims, block, kvh, 0, 0);
             float dot = 0.0f;
-            for (uint32_t d = 0; d < hd; ++d) dot += q_s[d] * bf16_bits_to_f32(kp[d]);
+            for (uint32_t d = 0; d < hd; ++d)
+                dot += q_s[d] * bf16_bits_to_f32(kp[k_tile_offset(dims, t, d)]);
             s = dot * scale;
         }
         slot_s[tid] = slot;

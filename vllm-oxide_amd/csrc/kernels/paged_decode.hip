@@ -10,12 +10,23 @@
 // scale*log2 e), fp32 accumulation, bf16 I/O.
 //
 // Work split.  The keys of each row are cut into splits of `split_keys`
-// (a multiple of 32).  Workgroup (item, k) owns one (row, split) for one KV
-// head and all G heads of its group, so every K/V byte is read from HBM once:
-// the algorithmic minimum.  Its W wavefronts take the split's 32-key chunks
-// round robin and merge through LDS at the end.  A row with one split writes
-// its bf16 output directly; otherwise the workgroup writes an fp32 partial
-// (m, l, acc[head_dim]) per head and decode_reduce_kernel merges them.
+// (a multiple of 32, at most kMaxSplitKeys).  Workgroup (item, k) owns one
+// (row, split) for one KV head and all G heads of its group, so every K/V
+// byte is read from HBM once: the algorithmic minimum.  The workgroup first
+// copies its split's block-table slice into LDS; its W wavefronts then take
+// the split's 32-key chunks round robin, each wavefront keeping the next
+// chunk's 16 loads in flight while it computes the current one (two register
+// buffers).  The wavefronts merge through LDS at the end.  A row with one
+// split writes its bf16 output directly; otherwise the workgroup writes an
+// fp32 partial (m, l, acc[head_dim]) per head, and decode_reduce_kernel
+// merges them:
+//   M = max_i m_i,  out = sum_i 2^(m_i-M) acc_i / sum_i 2^(m_i-M) l_i.
+// (Merging in the last workgroup to finish a row instead needs an
+// agent-scope release/acquire per workgroup; on gfx950 that is an L2
+// writeback and invalidate each time, which measured 5-9x slower than the
+// separate launch.)
+// Workgroups are numbered KV head fastest, so the KV heads of one block are
+// read at about the same time.
 //
 // One 32-key chunk (two 16-key blocks b0, b1) of one wavefront:
 //   Q.K^T: S^T[key, h] = K[key, :] . Q[h, :] with v_mfma_f32_16x16x32_bf16,
@@ -53,6 +64,7 @@ namespace {
 
 constexpr int kBS = 16;     // block size of the MFMA path
 constexpr int kChunk = 32;  // keys per wavefront iteration
+constexpr int kMaxSplitBlocks = kMaxSplitKeys / kBS;
 
 __device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -62,34 +74,146 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
 }
 
-template <int HD, int W>
-__global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
-    const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
-    uint32_t kv_heads, const uint32_t *__restrict__ table_off,
-    const uint32_t *__restrict__ tables, const uint32_t *__restrict__ row_seq,
-    const uint32_t *__restrict__ row_num_keys, const uint32_t *__restrict__ work,
-    const uint32_t *__restrict__ row_part, uint32_t split_keys,
-    const uint16_t *__restrict__ q, uint16_t *__restrict__ out, float *__restrict__ part_acc,
-    float *__restrict__ part_ml, uint32_t num_heads, uint32_t group, float scale_log2) {
-    constexpr int KK = HD / 32;  // QK MFMAs per 16 keys
-    constexpr int DT = HD / 16;  // PV output tiles
-    constexpr uint32_t kTile = kBS * HD;
+// One chunk's K and V operands, in registers.
+template <int HD>
+struct Chunk {
+    bf16x8 ka[HD / 32];  // first key set (keys 8g + 0..3 land in its result)
+    bf16x8 kb[HD / 32];  // second key set (keys 8g + 4..7)
+    bf16x8 va[HD / 16];  // V^T rows: dims 16*dt + l%16, keys 8g .. 8g+7
+};
 
-    const uint32_t item = blockIdx.x;
-    const uint32_t kvh = blockIdx.y;
+// Per-lane element offsets inside one (block, kv head) tile.  K tiles are
+// [head_dim/32][16 keys][32 dims] (vo_device.hpp).
+struct LaneMap {
+    uint32_t k_off;  // Q.K^T A-row m = l%16: key 8*((m>>2)&1) + (m&3), dims 8*(l/16)..
+    uint32_t v_off;  // P.V A-row d = l%16: keys 8*(g&1) .. +7 of block g>>1
+    bool k_hi;       // A-row m reads block b1 (m >= 8)
+    bool v_hi;       // lane group g reads block b1 (g >= 2)
+};
+
+template <int HD>
+__device__ __forceinline__ void load_chunk(Chunk<HD> &r, const uint16_t *k_head,
+                                           const uint16_t *v_head, uint64_t block_stride,
+                                           uint32_t phys0, uint32_t phys1, const LaneMap &lm) {
+    const uint16_t *kp =
+        k_head + static_cast<uint64_t>(lm.k_hi ? phys1 : phys0) * block_stride + lm.k_off;
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk) {
+        r.ka[kk] = load_bf16x8(kp + kk * (kBS * 32));
+        r.kb[kk] = load_bf16x8(kp + 4 * 32 + kk * (kBS * 32));
+    }
+    const uint16_t *vp =
+        v_head + static_cast<uint64_t>(lm.v_hi ? phys1 : phys0) * block_stride + lm.v_off;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) r.va[dt] = load_bf16x8(vp + dt * 16 * kBS);
+}
+
+// Online-softmax update with one chunk.  `nv` = valid keys of this lane's
+// group (0..8); the last chunk of a split passes tail = true.
+template <int HD>
+__device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 *qv, bool tail, int nv,
+                                              float scale_log2, float &m_run, float &l_run,
+                                              floatx4 *acc) {
+    floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < HD / 32; ++kk) {
+        s0 = mfma16x16x32(r.ka[kk], qv[kk], s0);
+        s1 = mfma16x16x32(r.kb[kk], qv[kk], s1);
+    }
+    float sc[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sc[i] = s0[i] * scale_log2;
+        sc[4 + i] = s1[i] * scale_log2;
+    }
+    if (tail) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc[i] = (i < nv) ? sc[i] : -INFINITY;
+        // Keys past the end get p = 0; zero their V too, so whatever the pool
+        // holds there cannot turn 0*x into NaN.
+        u32x4 mask;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            mask[p] = ((2 * p < nv) ? 0x0000ffffu : 0u) | ((2 * p + 1 < nv) ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt)
+            r.va[dt] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, r.va[dt]) & mask);
+    }
+    float mt = sc[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mt = fmaxf(mt, sc[i]);
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);  // finite: every chunk has a valid key
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    // P goes to the MFMA as two bf16 parts, hi = bf16(p) and lo = bf16(p - hi),
+    // so the probabilities keep ~16 significant bits instead of bf16's 8;
+    // bf16 P alone exceeds rtol 1e-2 / atol 2e-3 on rows whose weight sits on
+    // a few keys.
+    float ps = 0.0f;
+    bf16x8 pb_hi, pb_lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p = __builtin_amdgcn_exp2f(sc[i] - m_new);
+        ps += p;
+        const __bf16 hi = static_cast<__bf16>(p);
+        pb_hi[i] = hi;
+        pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+    }
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt) {
+        acc[dt] *= alpha;
+        acc[dt] = mfma16x16x32(r.va[dt], pb_lo, acc[dt]);
+        acc[dt] = mfma16x16x32(r.va[dt], pb_hi, acc[dt]);
+    }
+}
+
+template <int HD, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void
+decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
+                     uint32_t kv_heads, const uint32_t *__restrict__ table_off,
+                     const uint32_t *__restrict__ tables, const uint32_t *__restrict__ row_seq,
+                     const uint32_t *__restrict__ row_num_keys, const uint32_t *__restrict__ work,
+                     const uint32_t *__restrict__ row_info, uint32_t split_keys,
+                     const uint16_t *__restrict__ q, uint16_t *__restrict__ out,
+                     float *__restrict__ part_acc, float *__restrict__ part_ml, uint32_t num_heads,
+                     uint32_t group, float scale_log2) {
+    constexpr int KK = HD / 32;
+    constexpr int DT = HD / 16;
+    constexpr uint32_t kTile = kBS * HD;
+    __shared__ uint32_t s_table[kMaxSplitBlocks];
+
+    const uint32_t item = blockIdx.x / kv_heads;
+    const uint32_t kvh = blockIdx.x % kv_heads;
     const uint32_t row = work[2 * item];
     const uint32_t split = work[2 * item + 1];
-    const uint32_t seq = row_seq[row];
     const uint32_t nk = row_num_keys[row];
+    const uint64_t out_base = static_cast<uint64_t>(row) * num_heads * HD;
+
+    if (nk == 0) {
+        // The reference's empty softmax leaves the zero-filled output
+        // (attention.rs:119); one work item covers such a row.
+        for (uint32_t idx = threadIdx.x; idx < group * HD; idx += 64 * W)
+            out[out_base + static_cast<uint64_t>(kvh) * group * HD + idx] = 0;
+        return;
+    }
+
+    const uint32_t seq = row_seq[row];
     const uint32_t *table = tables + table_off[seq];
     const uint32_t k_begin = split * split_keys;
     const uint32_t k_end = min(nk, k_begin + split_keys);
     const uint32_t nsplit = (nk + split_keys - 1) / split_keys;
+    const uint32_t nblk = (k_end - k_begin + kBS - 1) / kBS;
+    const uint32_t lb0 = k_begin / kBS;
+
+    for (uint32_t i = threadIdx.x; i < nblk; i += 64 * W) s_table[i] = table[lb0 + i];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h = lane & 15;   // head column of this lane
-    const int g = lane >> 4;   // lane group: keys 8g..8g+7 of a chunk
+    const int h = lane & 15;  // head column of this lane
+    const int g = lane >> 4;  // lane group: keys 8g..8g+7 of a chunk
     const bool head_ok = h < static_cast<int>(group);
     const uint32_t qhead = kvh * group + h;
 
@@ -98,23 +222,20 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
     {
         const uint16_t *qp = q + (static_cast<uint64_t>(row) * num_heads + qhead) * HD + 8 * g;
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            if (head_ok)
-                qv[kk] = load_bf16x8(qp + 32 * kk);
-            else
-                qv[kk] = bf16x8{};
-        }
+        for (int kk = 0; kk < KK; ++kk) qv[kk] = head_ok ? load_bf16x8(qp + 32 * kk) : bf16x8{};
     }
 
-    // Q.K^T A-row assignment: row m = lane%16 reads block (m>>3) and key
-    // 8*((m>>2)&1) + (m&3) (+4 for the second key set).  With the MFMA output
-    // layout (lane l holds rows 4*(l/16)+i) this puts keys 8g+0..3 in the first
-    // result and 8g+4..7 in the second.
-    const int mrow = lane & 15;
-    const int k_sel = mrow >> 3;
-    const int k_t = 8 * ((mrow >> 2) & 1) + (mrow & 3);
-    const int v_sel = g >> 1;
-    const int v_t = 8 * (g & 1);
+    LaneMap lm;
+    {
+        const int m = lane & 15;
+        lm.k_off = (8 * ((m >> 2) & 1) + (m & 3)) * 32 + 8 * g;
+        lm.k_hi = m >= 8;
+        lm.v_off = m * kBS + 8 * (g & 1);
+        lm.v_hi = g >= 2;
+    }
+    const uint64_t block_stride = static_cast<uint64_t>(kv_heads) * kTile;
+    const uint16_t *k_head = k_pool + static_cast<uint64_t>(kvh) * kTile;
+    const uint16_t *v_head = v_pool + static_cast<uint64_t>(kvh) * kTile;
 
     float m_run = -INFINITY;
     float l_run = 0.0f;
@@ -122,85 +243,49 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    __syncthreads();  // s_table ready
+
     const uint32_t nchunks = (k_end - k_begin + kChunk - 1) / kChunk;
-    const uint64_t head_stride = static_cast<uint64_t>(kvh) * kTile;
-
-    for (uint32_t c = wave; c < nchunks; c += W) {
+    auto phys = [&](uint32_t c, uint32_t &p0, uint32_t &p1) {
+        p0 = s_table[2 * c];
+        p1 = (2 * c + 1 < nblk) ? s_table[2 * c + 1] : p0;
+    };
+    auto run = [&](Chunk<HD> &r, uint32_t c) {
         const uint32_t j0 = k_begin + c * kChunk;
-        const uint32_t lb = j0 / kBS;
-        const uint32_t phys0 = table[lb];
-        const uint32_t phys1 = (j0 + kBS < k_end) ? table[lb + 1] : phys0;
+        const bool tail = j0 + kChunk > k_end;
+        const int nv = max(0, min(8, static_cast<int>(k_end) - static_cast<int>(j0 + 8 * g)));
+        compute_chunk<HD>(r, qv, tail, nv, scale_log2, m_run, l_run, acc);
+    };
 
-        const uint32_t pk = k_sel ? phys1 : phys0;
-        const uint16_t *kp = k_pool + static_cast<uint64_t>(pk) * kv_heads * kTile + head_stride +
-                             k_t * HD + 8 * g;
-        bf16x8 ka[KK], kb[KK];
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            ka[kk] = load_bf16x8(kp + 32 * kk);
-            kb[kk] = load_bf16x8(kp + 4 * HD + 32 * kk);
-        }
-        const uint32_t pv = v_sel ? phys1 : phys0;
-        const uint16_t *vp = v_pool + static_cast<uint64_t>(pv) * kv_heads * kTile + head_stride +
-                             mrow * kBS + v_t;
-        bf16x8 va[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) va[dt] = load_bf16x8(vp + dt * 16 * kBS);
-
-        floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-            s0 = mfma16x16x32(ka[kk], qv[kk], s0);
-            s1 = mfma16x16x32(kb[kk], qv[kk], s1);
-        }
-
-        // Scores of keys j0 + 8g + i, i = 0..7.
-        const uint32_t jg = j0 + 8 * g;
-        float sc[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sc[i] = (jg + i < k_end) ? s0[i] * scale_log2 : -INFINITY;
-            sc[4 + i] = (jg + 4 + i < k_end) ? s1[i] * scale_log2 : -INFINITY;
-        }
-        float mt = sc[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) mt = fmaxf(mt, sc[i]);
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float m_new = fmaxf(m_run, mt);  // finite: the chunk has a valid key
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        // P goes to the MFMA as two bf16 parts, hi = bf16(p) and lo = bf16(p - hi),
-        // so the probabilities keep ~16 significant bits instead of bf16's 8;
-        // bf16 P alone exceeds rtol 1e-2 / atol 2e-3 on rows whose weight sits
-        // on a few keys.
-        float ps = 0.0f;
-        bf16x8 pb_hi, pb_lo;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float p = __builtin_amdgcn_exp2f(sc[i] - m_new);
-            ps += p;
-            const __bf16 hi = static_cast<__bf16>(p);
-            pb_hi[i] = hi;
-            pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
-        }
-        l_run = l_run * alpha + ps;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-
-        if (j0 + kChunk > k_end) {
-            // Tail chunk: keys past k_end have p = 0; zero their V as well so
-            // that whatever the pool holds there cannot turn 0*x into NaN.
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    if (jg + i >= k_end) va[dt][i] = static_cast<__bf16>(0.0f);
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            acc[dt] = mfma16x16x32(va[dt], pb_lo, acc[dt]);
-            acc[dt] = mfma16x16x32(va[dt], pb_hi, acc[dt]);
+    // Two register buffers: the loads of chunk c + W are in flight while
+    // chunk c is computed.  Each "load next; compute current" pair is
+    // straight-line code, so the compiler's wait before the compute covers
+    // only the current chunk's loads; the last chunk is computed without a
+    // prefetch.
+    Chunk<HD> bufA, bufB;
+    auto load = [&](Chunk<HD> &r, uint32_t cc) {
+        uint32_t p0, p1;
+        phys(cc, p0, p1);
+        load_chunk<HD>(r, k_head, v_head, block_stride, p0, p1, lm);
+    };
+    uint32_t c = wave;
+    if (c < nchunks) {
+        load(bufA, c);
+        for (;;) {
+            if (c + W >= nchunks) {
+                run(bufA, c);
+                break;
+            }
+            load(bufB, c + W);
+            run(bufA, c);
+            c += W;
+            if (c + W >= nchunks) {
+                run(bufB, c);
+                break;
+            }
+            load(bufA, c + W);
+            run(bufB, c);
+            c += W;
         }
     }
 
@@ -208,38 +293,38 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
 
-    const uint64_t out_base = static_cast<uint64_t>(row) * num_heads * HD;
-
+    const uint64_t part_base = static_cast<uint64_t>(row_info[2 * row] + split) * num_heads;
     if constexpr (W == 1) {
-        if (!head_ok) return;
-        if (nsplit == 1) {
-            const float inv = 1.0f / l_run;
-            uint16_t *op = out + out_base + static_cast<uint64_t>(qhead) * HD + 4 * g;
+        if (head_ok) {
+            if (nsplit == 1) {
+                const float inv = 1.0f / l_run;
+                uint16_t *op = out + out_base + static_cast<uint64_t>(qhead) * HD + 4 * g;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                u32x2 packed;
-                packed[0] = f32_to_bf16_bits(acc[dt][0] * inv) |
-                            (static_cast<uint32_t>(f32_to_bf16_bits(acc[dt][1] * inv)) << 16);
-                packed[1] = f32_to_bf16_bits(acc[dt][2] * inv) |
-                            (static_cast<uint32_t>(f32_to_bf16_bits(acc[dt][3] * inv)) << 16);
-                *reinterpret_cast<u32x2 *>(op + 16 * dt) = packed;
-            }
-        } else {
-            const uint64_t part = static_cast<uint64_t>(row_part[row] + split) * num_heads + qhead;
-            float *ap = part_acc + part * HD + 4 * g;
+                for (int dt = 0; dt < DT; ++dt) {
+                    u32x2 packed;
+                    packed[0] = f32_to_bf16_bits(acc[dt][0] * inv) |
+                                (static_cast<uint32_t>(f32_to_bf16_bits(acc[dt][1] * inv)) << 16);
+                    packed[1] = f32_to_bf16_bits(acc[dt][2] * inv) |
+                                (static_cast<uint32_t>(f32_to_bf16_bits(acc[dt][3] * inv)) << 16);
+                    *reinterpret_cast<u32x2 *>(op + 16 * dt) = packed;
+                }
+            } else {
+                const uint64_t part = part_base + qhead;
+                float *ap = part_acc + part * HD + 4 * g;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = acc[dt];
-            if (g == 0) {
-                part_ml[2 * part] = m_run;
-                part_ml[2 * part + 1] = l_run;
+                for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = acc[dt];
+                if (g == 0) {
+                    part_ml[2 * part] = m_run;
+                    part_ml[2 * part + 1] = l_run;
+                }
             }
         }
     } else {
         // Merge the W wavefronts' (m, l, acc) through LDS.
         extern __shared__ float smem[];
-        float *sm_m = smem;                  // [W][16]
-        float *sm_l = sm_m + W * 16;         // [W][16]
-        float *sm_acc = sm_l + W * 16;       // [W][group][HD]
+        float *sm_m = smem;             // [W][16]
+        float *sm_l = sm_m + W * 16;    // [W][16]
+        float *sm_acc = sm_l + W * 16;  // [W][group][HD]
         if (head_ok) {
             if (g == 0) {
                 sm_m[wave * 16 + h] = m_run;
@@ -250,8 +335,7 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = acc[dt];
         }
         __syncthreads();
-        const uint32_t total = group * HD;
-        for (uint32_t idx = threadIdx.x; idx < total; idx += 64 * W) {
+        for (uint32_t idx = threadIdx.x; idx < group * HD; idx += 64 * W) {
             const uint32_t hh = idx / HD;
             const uint32_t d = idx % HD;
             float mx = -INFINITY;
@@ -271,7 +355,7 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
             if (nsplit == 1) {
                 out[out_base + static_cast<uint64_t>(qh) * HD + d] = f32_to_bf16_bits(num / den);
             } else {
-                const uint64_t part = static_cast<uint64_t>(row_part[row] + split) * num_heads + qh;
+                const uint64_t part = part_base + qh;
                 part_acc[part * HD + d] = num;
                 if (d == 0) {
                     part_ml[2 * part] = mx;
@@ -282,43 +366,48 @@ __global__ __launch_bounds__(64 * W) void decode_splitk_kernel(
     }
 }
 
-// Merge the split-K partials of one (row, head):
-//   M = max_i m_i,  out = sum_i 2^(m_i - M) acc_i / sum_i 2^(m_i - M) l_i
-// (log2 domain, matching the split kernel).  Rows with one split were
-// written by the split kernel; rows with zero keys get zeros (the
-// reference's empty softmax leaves the zero-filled output, attention.rs:119).
+// Merge the split-K partials of one (row, KV head) for the G query heads of
+// its group; rows with one split were written by the split kernel.  Each
+// thread owns 4 consecutive dims of one head and folds the splits in with a
+// running max, so all of its loads are independent of each other.
 template <int HD>
-__global__ __launch_bounds__(64) void decode_reduce_kernel(
-    const uint32_t *__restrict__ row_num_keys, const uint32_t *__restrict__ row_part,
-    uint32_t split_keys, const float *__restrict__ part_acc, const float *__restrict__ part_ml,
-    uint16_t *__restrict__ out, uint32_t num_heads) {
-    const uint32_t row = blockIdx.x;
-    const uint32_t head = blockIdx.y;
-    const uint32_t nk = row_num_keys[row];
-    const uint32_t nsplit = (nk + split_keys - 1) / split_keys;
-    if (nsplit == 1) return;
-    uint16_t *op = out + (static_cast<uint64_t>(row) * num_heads + head) * HD;
-    if (nsplit == 0) {
-        for (uint32_t d = threadIdx.x; d < HD; d += 64) op[d] = 0;
-        return;
+__global__ __launch_bounds__(128) void decode_reduce_kernel(
+    const uint32_t *__restrict__ row_info, const float *__restrict__ part_acc,
+    const float *__restrict__ part_ml, uint16_t *__restrict__ out, uint32_t num_heads,
+    uint32_t kv_heads, uint32_t group) {
+    const uint32_t row = blockIdx.x / kv_heads;
+    const uint32_t kvh = blockIdx.x % kv_heads;
+    const uint32_t first = row_info[2 * row];
+    const uint32_t nsplit = row_info[2 * row + 1];
+    if (nsplit <= 1) return;
+    const uint64_t out_base = static_cast<uint64_t>(row) * num_heads * HD;
+    for (uint32_t idx = threadIdx.x; idx < group * (HD / 4); idx += 128) {
+        const uint32_t qh = kvh * group + idx / (HD / 4);
+        const uint32_t d = 4 * (idx % (HD / 4));
+        const uint64_t p0 = static_cast<uint64_t>(first) * num_heads + qh;
+        float mx = -INFINITY, den = 0.0f;
+        floatx4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (uint32_t i = 0; i < nsplit; ++i) {
+            const uint64_t p = p0 + static_cast<uint64_t>(i) * num_heads;
+            const float m = part_ml[2 * p];
+            const float l = part_ml[2 * p + 1];
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(part_acc + p * HD + d);
+            const float m_new = fmaxf(mx, m);
+            const float scale_old = __builtin_amdgcn_exp2f(mx - m_new);
+            const float e = __builtin_amdgcn_exp2f(m - m_new);
+            den = den * scale_old + e * l;
+            num = num * scale_old + a * e;
+            mx = m_new;
+        }
+        const float inv = 1.0f / den;
+        u32x2 packed;
+        packed[0] = f32_to_bf16_bits(num[0] * inv) |
+                    (static_cast<uint32_t>(f32_to_bf16_bits(num[1] * inv)) << 16);
+        packed[1] = f32_to_bf16_bits(num[2] * inv) |
+                    (static_cast<uint32_t>(f32_to_bf16_bits(num[3] * inv)) << 16);
+        *reinterpret_cast<u32x2 *>(out + out_base + static_cast<uint64_t>(qh) * HD + d) = packed;
     }
-    const uint64_t p0 = static_cast<uint64_t>(row_part[row]) * num_heads + head;
-    float mx = -INFINITY;
-    for (uint32_t i = 0; i < nsplit; ++i) mx = fmaxf(mx, part_ml[2 * (p0 + i * num_heads)]);
-    float den = 0.0f;
-    float num[HD / 64];
-#pragma unroll
-    for (int r = 0; r < HD / 64; ++r) num[r] = 0.0f;
-    for (uint32_t i = 0; i < nsplit; ++i) {
-        const uint64_t p = p0 + static_cast<uint64_t>(i) * num_heads;
-        const float e = __builtin_amdgcn_exp2f(part_ml[2 * p] - mx);
-        den += e * part_ml[2 * p + 1];
-#pragma unroll
-        for (int r = 0; r < HD / 64; ++r) num[r] += e * part_acc[p * HD + threadIdx.x + 64 * r];
-    }
-    const float inv = 1.0f / den;
-#pragma unroll
-    for (int r = 0; r < HD / 64; ++r) op[threadIdx.x + 64 * r] = f32_to_bf16_bits(num[r] * inv);
 }
 
 template <int HD, int W>
@@ -327,10 +416,12 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                         hipStream_t stream) {
     const uint32_t group = num_heads / pool.kv_heads;
     const size_t smem = (W == 1) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * group * HD) * 4;
+    const uint64_t grid = static_cast<uint64_t>(plan.num_work) * pool.kv_heads;
+    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
-    hipLaunchKernelGGL((decode_splitk_kernel<HD, W>), dim3(plan.num_work, pool.kv_heads),
+    hipLaunchKernelGGL((decode_splitk_kernel<HD, W>), dim3(static_cast<uint32_t>(grid)),
                        dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
-                       meta.tables, meta.row_seq, meta.row_num_keys, plan.work, plan.row_part,
+                       meta.tables, meta.row_seq, meta.row_num_keys, plan.work, plan.row_info,
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
                        scale_log2);
     return hipGetLastError();
@@ -340,20 +431,20 @@ template <int HD>
 hipError_t launch_hd(const PoolLayer &pool, const MetaView &meta, const DecodePlan &plan,
                      const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
                      int waves, hipStream_t stream) {
-    hipError_t err = hipSuccess;
-    if (plan.num_work > 0) {
-        switch (waves) {
-            case 1: err = launch_split<HD, 1>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
-            case 2: err = launch_split<HD, 2>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
-            default: err = launch_split<HD, 4>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
-        }
-        if (err != hipSuccess) return err;
+    hipError_t err;
+    switch (waves) {
+        case 1: err = launch_split<HD, 1>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
+        case 2: err = launch_split<HD, 2>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
+        case 8: err = launch_split<HD, 8>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
+        default: err = launch_split<HD, 4>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
     }
-    if (!plan.needs_reduce) return hipSuccess;
+    if (err != hipSuccess || !plan.needs_reduce) return err;
+    const uint64_t grid = static_cast<uint64_t>(meta.num_rows) * pool.kv_heads;
+    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_reduce", stream);
-    hipLaunchKernelGGL((decode_reduce_kernel<HD>), dim3(meta.num_rows, num_heads), dim3(64), 0,
-                       stream, meta.row_num_keys, plan.row_part, plan.split_keys, plan.part_acc,
-                       plan.part_ml, out, num_heads);
+    hipLaunchKernelGGL((decode_reduce_kernel<HD>), dim3(static_cast<uint32_t>(grid)), dim3(128),
+                       0, stream, plan.row_info, plan.part_acc, plan.part_ml, out, num_heads,
+                       pool.kv_heads, num_heads / pool.kv_heads);
     return hipGetLastError();
 }
 
@@ -367,12 +458,19 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               const DecodePlan &plan, const uint16_t *q, uint16_t *out,
                               uint32_t num_heads, float scale, int waves_per_group,
                               hipStream_t stream) {
-    if (meta.num_rows == 0) return hipSuccess;
+    if (meta.num_rows == 0 || plan.num_work == 0) return hipSuccess;
+    if (plan.split_keys == 0 || plan.split_keys % kChunk != 0 || plan.split_keys > kMaxSplitKeys)
+        return hipErrorInvalidValue;
     const float scale_log2 = scale * 1.4426950408889634f;
     switch (pool.head_dim) {
-        case 64: return launch_hd<64>(pool, meta, plan, q, out, num_heads, scale_log2, waves_per_group, stream);
-        case 128: return launch_hd<128>(pool, meta, plan, q, out, num_heads, scale_log2, waves_per_group, stream);
-        default: return hipErrorInvalidValue;
+        case 64:
+            return launch_hd<64>(pool, meta, plan, q, out, num_heads, scale_log2, waves_per_group,
+                                 stream);
+        case 128:
+            return launch_hd<128>(pool, meta, plan, q, out, num_heads, scale_log2,
+                                  waves_per_group, stream);
+        default:
+            return hipErrorInvalidValue;
     }
 }
 

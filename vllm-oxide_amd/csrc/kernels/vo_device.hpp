@@ -3,14 +3,17 @@
 // Pool layout (backend-private; the reference leaves the bytes to the
 // backend, crates/engine/src/backend/mod.rs:10-12).  Per layer:
 //
-//   K: [num_blocks][kv_heads][block_size][head_dim]   bf16   ("key-major tile")
-//   V: [num_blocks][kv_heads][head_dim][block_size]   bf16   ("dim-major tile")
+//   K: [num_blocks][kv_heads][head_dim/CW][block_size][CW]  bf16  ("key-major tile")
+//   V: [num_blocks][kv_heads][head_dim][block_size]         bf16  ("dim-major tile")
 //
-// One (block, kv_head) tile is block_size*head_dim*2 bytes contiguous for K
-// and for V (4 KiB at bs 16, hd 128).  K keeps a key's head_dim values
-// together, which is the row operand of the Q.K^T MFMA; V keeps a dim's
-// block_size keys together, which is the row operand of the V^T.P MFMA.
-// The logical slot semantics are the reference's: slot = block*bs + offset
+// with CW = 32 dims when head_dim is a multiple of 32, else 8.  One
+// (block, kv_head) tile is block_size*head_dim*2 bytes contiguous for K and
+// for V (4 KiB at bs 16, hd 128).  K keeps 32 consecutive dims of a key
+// together (64 bytes), the row operand of one Q.K^T MFMA step, and puts the
+// block's keys for the same 32 dims next to each other, so one load
+// instruction of the decode kernel reads whole 128-byte lines; V keeps a
+// dim's block_size keys together, the row operand of the V^T.P MFMA.  The
+// logical slot semantics are the reference's: slot = block*bs + offset
 // (crates/engine/src/backend/paged.rs:25-28).
 #pragma once
 
@@ -43,11 +46,23 @@ struct PoolDims {
     uint32_t block_size;
 };
 
-// Element offset of K[block][kvh][t][d] within one layer's K region.
+// Dims per K chunk (see the layout above).
+__host__ __device__ __forceinline__ uint32_t k_chunk_dims(uint32_t head_dim) {
+    return (head_dim % 32 == 0) ? 32u : 8u;
+}
+
+// Element offset of key t, dim d inside one K tile.  Eight consecutive dims
+// starting at a multiple of 8 are contiguous.
+__device__ __forceinline__ uint32_t k_tile_offset(const PoolDims &p, uint32_t t, uint32_t d) {
+    const uint32_t cw = k_chunk_dims(p.head_dim);
+    return (d / cw) * (p.block_size * cw) + t * cw + d % cw;
+}
+
+// Element offset of K[block][kvh][key t][dim d] within one layer's K region.
 __device__ __forceinline__ uint64_t k_offset(const PoolDims &p, uint32_t block, uint32_t kvh,
                                              uint32_t t, uint32_t d) {
     return (static_cast<uint64_t>(block) * p.kv_heads + kvh) * (p.block_size * p.head_dim) +
-           static_cast<uint64_t>(t) * p.head_dim + d;
+           k_tile_offset(p, t, d);
 }
 
 // Element offset of V[block][kvh][d][t] within one layer's V region.

@@ -66,21 +66,25 @@ hipError_t launch_attention_generic(const PoolLayer &pool, const MetaView &meta,
                                     const uint16_t *q, uint16_t *out, uint32_t num_heads,
                                     float scale, hipStream_t stream);
 
+// Largest split the decode kernel takes (its block-table slice lives in LDS).
+constexpr uint32_t kMaxSplitKeys = 4096;
+
 // Split-K work plan for the MFMA decode kernel.
 struct DecodePlan {
-    const uint32_t *work;         // [num_work][2]: (row, split)
-    const uint32_t *row_part;     // [T]: first partial index of each row
+    const uint32_t *work;         // [num_work][2]: (row, split); a zero-key row has one item
+    const uint32_t *row_info;     // [T][2]: (first partial index, number of splits)
     uint32_t num_work;
-    uint32_t split_keys;          // keys per split, a multiple of 32
+    uint32_t split_keys;          // keys per split, a multiple of 32, <= kMaxSplitKeys
     float *part_acc;              // [parts][num_heads][head_dim]
     float *part_ml;               // [parts][num_heads][2]: (max, sum), log2 domain
-    bool needs_reduce;            // some row has zero keys or more than one split
+    bool needs_reduce;            // some row has more than one split
 };
 
 // True when the MFMA decode kernel covers this shape.
 bool decode_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t group);
 
-// MFMA split-K decode (one launch) + reduce (one launch).
+// MFMA split-K decode (one launch) and, when a row has several splits, the
+// reduce kernel (a second launch).
 hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               const DecodePlan &plan, const uint16_t *q, uint16_t *out,
                               uint32_t num_heads, float scale, int waves_per_group,

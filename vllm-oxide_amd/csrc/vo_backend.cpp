@@ -352,28 +352,34 @@ constexpr uint64_t kDefaultSplit = 512;
 
 uint64_t decode_split_keys() {
     const int env = env_int("VO_DECODE_SPLIT", 0);
-    return (env >= 32 && env % 32 == 0) ? static_cast<uint64_t>(env) : kDefaultSplit;
+    return (env >= 32 && env % 32 == 0 && env <= static_cast<int>(kernels::kMaxSplitKeys))
+               ? static_cast<uint64_t>(env)
+               : kDefaultSplit;
 }
+
+// Rows with zero keys still get one work item (it writes the zero output).
+uint64_t row_splits(uint64_t keys, uint64_t L) { return keys ? (keys + L - 1) / L : 1; }
 
 vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
     const uint64_t T = m->num_rows;
     const uint64_t L = decode_split_keys();
     uint64_t parts = 0;
-    for (uint64_t r = 0; r < T; ++r) parts += (m->row_num_keys[r] + L - 1) / L;
+    for (uint64_t r = 0; r < T; ++r) parts += row_splits(m->row_num_keys[r], L);
     if (parts > m->max_parts) return fail_capacity("split-K partials per step", parts, m->max_parts);
     (void)op;
 
     const uint32_t *dp;
     uint32_t *work = pk.add(2 * parts, &dp);
     m->plan.work = dp;
-    uint32_t *row_part = pk.add(T, &dp);
-    m->plan.row_part = dp;
+    uint32_t *row_info = pk.add(2 * T, &dp);
+    m->plan.row_info = dp;
     uint64_t n = 0;
     bool needs_reduce = false;
     for (uint64_t r = 0; r < T; ++r) {
-        const uint64_t ns = (m->row_num_keys[r] + L - 1) / L;
-        row_part[r] = static_cast<uint32_t>(n);
-        if (ns != 1) needs_reduce = true;
+        const uint64_t ns = row_splits(m->row_num_keys[r], L);
+        row_info[2 * r] = static_cast<uint32_t>(n);
+        row_info[2 * r + 1] = static_cast<uint32_t>(ns);
+        if (ns > 1) needs_reduce = true;
         for (uint64_t s = 0; s < ns; ++s, ++n) {
             work[2 * n] = static_cast<uint32_t>(r);
             work[2 * n + 1] = static_cast<uint32_t>(s);
@@ -390,8 +396,9 @@ vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
 
 int decode_waves() {
     int w = env_int("VO_DECODE_WAVES", 4);
-    return (w == 1 || w == 2 || w == 4) ? w : 4;
+    return (w == 1 || w == 2 || w == 4 || w == 8) ? w : 4;
 }
+
 
 }  // namespace
 
@@ -426,7 +433,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
 
     const uint64_t u32s = (max_seqs + 1) + max_table_entries + 3 * max_rows  // offsets, tables, row arrays
                           + max_rows                                         // write slots
-                          + 2 * m->max_parts + max_rows                      // decode plan
+                          + 2 * m->max_parts + 2 * max_rows                  // decode plan
                           + 8 * 64;                                          // alignment slack
     m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
     hipError_t err = hipMalloc(reinterpret_cast<void **>(&m->d_buf), m->buf_bytes);
