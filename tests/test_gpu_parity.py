@@ -272,8 +272,11 @@ def test_decode_block_relabelling_invariance_bitwise(vo, gpu_backend):
 # ---------------------------------------------------------------------------
 # Prefill
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("hd,heads,kvh", [(128, 32, 8), (64, 4, 2)])
+@pytest.mark.parametrize("hd,heads,kvh", [(128, 32, 8), (64, 4, 2), (128, 64, 8), (128, 16, 8),
+                                          (64, 12, 3)])
 def test_prefill_chunked_with_context(vo, gpu_backend, hd, heads, kvh):
+    """Chunks that start at position 0, mid-block and on block boundaries;
+    chunk lengths of 1, non-multiples of the 32-row tile, and > 64 rows."""
     _say(f"prefill hd={hd} heads={heads}")
     wl = W.build(vo, gpu_backend, kind="prefill", heads=heads, kv_heads=kvh, head_dim=hd,
                  block_size=16, num_blocks=800, context_lens=[0, 37, 256, 1000, 5],

@@ -90,5 +90,21 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               uint32_t num_heads, float scale, int waves_per_group,
                               hipStream_t stream);
 
+// Work plan of the MFMA prefill kernel: one item per 32-row query tile of a
+// sequence, longest first.
+struct PrefillPlan {
+    const uint32_t *work;  // [num_items][4]: (first row, rows, position of first row, sequence)
+    uint32_t num_items;
+};
+
+// True when the MFMA prefill kernel covers this shape.
+bool prefill_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t group);
+// Query rows per work item of the MFMA prefill kernel.
+uint32_t prefill_rows_per_tile();
+
+hipError_t launch_prefill_mfma(const PoolLayer &pool, const MetaView &meta,
+                               const PrefillPlan &plan, const uint16_t *q, uint16_t *out,
+                               uint32_t num_heads, float scale, hipStream_t stream);
+
 }  // namespace kernels
 }  // namespace vo

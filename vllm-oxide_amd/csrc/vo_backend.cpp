@@ -180,6 +180,8 @@ struct vo_step_meta {
     const uint32_t *d_write_slots = nullptr;  // slots with superseded rows = kSkipSlot
     kernels::DecodePlan plan{};
     bool decode_planned = false;
+    kernels::PrefillPlan prefill_plan{};
+    bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
 };
 
 namespace {
@@ -394,6 +396,52 @@ vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
     return VO_OK;
 }
 
+// Prefill plan for the MFMA kernel: one item per 32-row query tile.  It needs
+// the layout PrefillMeta::new produces (paged.rs:128-141): the rows of
+// sequence s are seq_row_starts[s] .. seq_row_starts[s+1], row i of them at
+// position context_lens[s] + i with i + 1 + context_lens[s] keys.  Other
+// layouts run on the generic kernel.  Items are sorted by KV tiles, longest
+// first, so that the long ones are scheduled early.
+void plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens,
+                  const uint64_t *seq_row_starts) {
+    m->prefill_planned = false;
+    const uint64_t S = m->num_seqs;
+    for (uint64_t s = 0; s < S; ++s) {
+        for (uint64_t r = seq_row_starts[s]; r < seq_row_starts[s + 1]; ++r) {
+            const uint64_t i = r - seq_row_starts[s];
+            if (m->row_seq[r] != s || m->row_num_keys[r] != context_lens[s] + i + 1) return;
+        }
+    }
+    const uint32_t QT = kernels::prefill_rows_per_tile();
+    struct Item { uint32_t row, rows, pos, seq, tiles; };
+    std::vector<Item> items;
+    for (uint64_t s = 0; s < S; ++s) {
+        const uint64_t n = seq_row_starts[s + 1] - seq_row_starts[s];
+        for (uint64_t q0 = 0; q0 < n; q0 += QT) {
+            Item it;
+            it.row = static_cast<uint32_t>(seq_row_starts[s] + q0);
+            it.rows = static_cast<uint32_t>(std::min<uint64_t>(QT, n - q0));
+            it.pos = static_cast<uint32_t>(context_lens[s] + q0);
+            it.seq = static_cast<uint32_t>(s);
+            it.tiles = (it.pos + it.rows - 1) / 64 + 1;
+            items.push_back(it);
+        }
+    }
+    std::stable_sort(items.begin(), items.end(),
+                     [](const Item &a, const Item &b) { return a.tiles > b.tiles; });
+    const uint32_t *dp;
+    uint32_t *w = pk.add(4 * items.size(), &dp);
+    for (size_t i = 0; i < items.size(); ++i) {
+        w[4 * i] = items[i].row;
+        w[4 * i + 1] = items[i].rows;
+        w[4 * i + 2] = items[i].pos;
+        w[4 * i + 3] = items[i].seq;
+    }
+    m->prefill_plan.work = dp;
+    m->prefill_plan.num_items = static_cast<uint32_t>(items.size());
+    m->prefill_planned = true;
+}
+
 int decode_waves() {
     int w = env_int("VO_DECODE_WAVES", 4);
     return (w == 1 || w == 2 || w == 4 || w == 8) ? w : 4;
@@ -434,6 +482,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
     const uint64_t u32s = (max_seqs + 1) + max_table_entries + 3 * max_rows  // offsets, tables, row arrays
                           + max_rows                                         // write slots
                           + 2 * m->max_parts + 2 * max_rows                  // decode plan
+                          + 4 * (max_rows + max_seqs)                        // prefill plan
                           + 8 * 64;                                          // alignment slack
     m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
     hipError_t err = hipMalloc(reinterpret_cast<void **>(&m->d_buf), m->buf_bytes);
@@ -492,6 +541,7 @@ extern "C" int32_t vo_step_meta_upload_prefill(
     if (vo_status rc = upload_common(m, kPrefill, op, block_size, num_seqs, table_off, tables,
                                      num_rows, slot_mapping, row_seq, row_num_keys, pk))
         return rc;
+    plan_prefill(m, pk, context_lens, seq_row_starts);
     if (!pk.fits()) {
         m->kind = kNone;
         return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
@@ -669,10 +719,21 @@ extern "C" int32_t vo_prefill_attention(const void *queries, uint64_t rows, uint
     const vo_kv_layout &L = pool->layout;
     const uint32_t heads = static_cast<uint32_t>(cols / L.head_dim);
     const float scale = 1.0f / std::sqrt(static_cast<float>(L.head_dim));  // attention.rs:88
+    const uint32_t group = heads / static_cast<uint32_t>(L.kv_heads);
     DeviceGuard guard(pool->device);
-    hipError_t err = kernels::launch_attention_generic(
-        pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),
-        static_cast<uint16_t *>(out), heads, scale, static_cast<hipStream_t>(stream));
+    hipError_t err;
+    if (m->prefill_planned &&
+        kernels::prefill_mfma_supported(static_cast<uint32_t>(L.head_dim),
+                                        static_cast<uint32_t>(L.block_size), group)) {
+        err = kernels::launch_prefill_mfma(pool->layer(layer), m->view, m->prefill_plan,
+                                           static_cast<const uint16_t *>(queries),
+                                           static_cast<uint16_t *>(out), heads, scale,
+                                           static_cast<hipStream_t>(stream));
+    } else {
+        err = kernels::launch_attention_generic(
+            pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),
+            static_cast<uint16_t *>(out), heads, scale, static_cast<hipStream_t>(stream));
+    }
     return device_status(op, err);
 }
 
