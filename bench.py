@@ -64,14 +64,23 @@ def cpu_info():
 
 def traffic_record(kernel, workload):
     """Counter-measured HBM bytes per launch, from the committed rocprofv3
-    --pmc summary for this kernel and workload (profiles/*.json), or None."""
+    --pmc summary for this kernel and workload (profiles/*.json), or None.
+    A record counts only while the kernel source it was measured on is
+    unchanged (sha256 prefix of the source file)."""
+    import hashlib
     for p in sorted((ROOT / "profiles").glob("*.json")):
         try:
             rec = json.loads(p.read_text())
         except (OSError, ValueError):
             continue
-        if rec.get("kernel") == kernel and rec.get("workload") == workload:
-            return rec.get("hbm_bytes_per_launch")
+        if rec.get("kernel") != kernel or rec.get("workload") != workload:
+            continue
+        src = ROOT / rec.get("source", "")
+        if not src.is_file():
+            continue
+        if hashlib.sha256(src.read_bytes()).hexdigest()[:16] != rec.get("source_sha256_16"):
+            continue
+        return rec.get("hbm_bytes_per_launch")
     return None
 
 
