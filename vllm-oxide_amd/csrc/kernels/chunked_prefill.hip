@@ -7,15 +7,21 @@
 // cached context is fully visible and the chunk is causal because row t is
 // given only p + 1 keys (attention.rs:16).
 //
-// Work split.  A workgroup owns one 32-row query tile of one sequence and one
-// KV head k, with one wavefront per query head of k's GQA group (G waves), so
-// every K/V tile staged in LDS serves all G heads.  It walks the 64-key KV
-// tiles 0 .. p_max/64 of its sequence; tiles past the tile's last row are
-// never touched, tiles wholly before its first row need no mask.  Work items
-// are ordered longest first (host plan), so the long tiles start early.
+// Work split.  A work item is a 64-row query tile of one sequence (host
+// plan, longest first).  A workgroup owns R 32-row groups of one item and one
+// KV head k, with one wavefront per (row group, query head of k's GQA group):
+// R = 2 for groups up to 4 heads (8 waves), R = 1 with two workgroups per item
+// for 8 heads, so that every K/V tile staged in LDS serves 64 rows x G heads
+// and the pool is read once per 64 query rows.  The workgroup walks the
+// 64-key KV tiles 0 .. p_max/64 of its sequence; tiles past its last row are
+// never touched, tiles wholly before a wave's first row need no mask.  The
+// grid runs KV heads fastest: workgroups are dealt to the 8 XCDs round-robin,
+// so with 8 (or 16 ..) KV heads every (sequence, KV head) stream stays in one
+// XCD's L2 and its q tiles, which walk the same KV tiles at the same pace,
+// share the loads.
 //
 // Per wavefront and KV tile (keys j0 .. j0+63), with c = lane % 32 the query
-// row of the lane and gl = lane / 32:
+// row of the lane within its row group and gl = lane / 32:
 //   S^T = K . Q^T    v_mfma_f32_32x32x16_bf16, A = 32 keys x 16 dims of K
 //                    from LDS, B = Q^T (the wave's 32 query rows, kept in
 //                    registers for the whole kernel); two 32-key halves,
@@ -23,23 +29,37 @@
 //                    swap of bits 2 and 3, so that the result register r of
 //                    lane l holds key 32*half + 16*(r>>3) + 8*gl + (r&7).
 //   softmax          each lane holds 32 scores of its own query row; the row
-//                    max is a local max plus one lane^32 exchange.
+//                    max is a local max plus one lane^32 exchange.  The
+//                    probabilities are exp2(s*scale*log2e - m) with m a
+//                    running row max that is only raised when the tile max
+//                    exceeds it by more than kLazyLog2 (the accumulators are
+//                    rescaled then); otherwise the tile reuses the stale m,
+//                    which leaves numerator and denominator scaled alike and
+//                    keeps P <= 2^kLazyLog2.
 //   O^T += V^T . P^T B = P^T is then exactly the lane's own probabilities:
 //                    16-key step j uses registers 8*(j&1) .. +7 of half j>>1.
 //                    A = 32 dims x 16 keys of V^T from LDS.  Output rows are
-//                    dims and columns query rows, so the rescale by the new
-//                    max is lane-local.  The first KV tile, where rows with
-//                    few keys live, feeds P as bf16 hi + lo parts (two
-//                    MFMAs) so that short rows keep rtol 1e-2 / atol 2e-3.
+//                    dims and columns query rows, so the rescale is
+//                    lane-local.  Tile 0, where rows with few keys live,
+//                    feeds P as bf16 hi + lo parts (two MFMAs) so that short
+//                    rows keep rtol 1e-2 / atol 2e-3; later tiles feed the
+//                    rounded P and sum the same rounded values into the
+//                    denominator (v_dot2c_f32_bf16).
 //
-// LDS: K tile [64 keys][head_dim] and V^T tile [head_dim][64 keys], 16-byte
-// units XOR-swizzled by row so that the 16 lanes of one ds_read_b128 phase
-// hit 16 different 16-byte slots of a 256-byte bank sweep; two buffers, the
-// next tile's global loads are in flight while the current one is computed.
+// Staging.  A KV tile is 4 blocks x head_dim/32 (block, 32-dim chunk) pairs of
+// 1 KiB for K and for V; each wave loads whole pairs (64 lanes x 16 bytes,
+// contiguous in the pool) into registers and writes them to LDS after the
+// current tile's MFMAs.  LDS rows are padded by 16 bytes (K: [64 keys]
+// [head_dim + 8], V^T: [head_dim][64 + 8 keys]) so that the 16 lanes of a
+// ds_read_b128 phase cover all 64 banks; two buffers, one barrier per tile.
+// The block-table entries of tile t+2 are loaded while tile t is computed
+// (lane b < 4 holds block b of the tile) and broadcast with v_readlane, so the
+// K/V load addresses of the next tile are scalar and ready.
 //
 // Roofline: bf16 MFMA.  Algorithmic FLOPs = sum over rows of (keys) * heads *
 // 4 * head_dim (Q.K^T and P.V, causal-aware).
 #include <cmath>
+#include <type_traits>
 
 #include "vo_device.hpp"
 #include "vo_kernels.hpp"
@@ -49,21 +69,16 @@ namespace kernels {
 
 namespace {
 
-constexpr int kBS = 16;  // block size of the MFMA path
-constexpr int kQT = 32;  // query rows per tile
-constexpr int kKT = 64;  // keys per KV tile (4 blocks)
+constexpr int kBS = 16;          // block size of the MFMA path
+constexpr int kQT = 64;          // query rows per work item
+constexpr int kRG = 32;          // query rows per wavefront
+constexpr int kKT = 64;          // keys per KV tile (4 blocks)
+constexpr float kLazyLog2 = 8.0f;  // growth of a row max (log2 units) absorbed without a rescale
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ floatx16 mfma32x32x16(bf16x8 a, bf16x8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// 16-byte slot of unit u in LDS row `row` (see the header comment).
-template <int UNITS_PER_ROW>
-__device__ __forceinline__ uint32_t swizzle(uint32_t u, uint32_t row) {
-    if constexpr (UNITS_PER_ROW == 16)
-        return u ^ (row & 15u);
-    else
-        return u ^ ((row >> 1) & 7u);
 }
 
 // Swap bits 2 and 3: the A-row -> key order of the Q.K^T MFMA.
@@ -71,31 +86,65 @@ __device__ __forceinline__ uint32_t key_perm(uint32_t i) {
     return (i & ~0xCu) | ((i & 4u) << 1) | ((i & 8u) >> 1);
 }
 
-template <int HD, int G>
-__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2))) void prefill_mfma_kernel(
+// Sum of the eight bf16 values of v, accumulated onto acc in fp32.
+__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
+    const bf16x2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), one, acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
+}
+
+template <int HD, int W>
+struct TileShape {
+    static constexpr int KS = HD / 16;               // Q.K^T k-steps
+    static constexpr int DT = HD / 32;               // P.V output tiles (32 dims)
+    static constexpr int CH = HD / 32;               // 32-dim chunks of a block tile
+    static constexpr int KSTR = HD * 2 + 16;         // bytes per K row in LDS
+    static constexpr int VSTR = kKT * 2 + 16;        // bytes per V^T row in LDS
+    static constexpr int KBYTES = kKT * KSTR;
+    static constexpr int BUF = KBYTES + HD * VSTR;   // one K + V^T buffer
+    static constexpr int PAIRS = (kKT / kBS) * CH;   // (block, chunk) pairs per tile
+    static constexpr int UPT = PAIRS / W;            // pairs per wave per tile
+    static_assert(PAIRS % W == 0, "pairs must divide over the waves");
+
+    // Pair i of wave w: block b of the tile and 32-dim chunk ch, both
+    // wave-uniform; the waves of one step cover distinct pairs.
+    __device__ static __forceinline__ void pair(uint32_t w, int i, uint32_t &b, uint32_t &ch) {
+        if constexpr (W >= CH) {
+            b = w / CH + (W / CH) * i;
+            ch = w % CH;
+        } else {
+            b = i / (CH / W);
+            ch = w + W * (i % (CH / W));
+        }
+    }
+};
+
+template <int HD, int G, int R>
+__global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2))) void prefill_mfma_kernel(
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
     const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
-    const uint32_t *__restrict__ work, uint32_t num_items, const uint16_t *__restrict__ q,
+    const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
     uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2) {
-    constexpr int KS = HD / 16;                 // Q.K^T k-steps
-    constexpr int DT = HD / 32;                 // P.V output tiles
-    constexpr int KROW = HD * 2;                // bytes of one K row in LDS
-    constexpr int KUPR = HD / 8;                // 16-byte units per K row
-    constexpr int TILE_BYTES = kKT * HD * 2;    // K (or V) tile in LDS
-    constexpr int UNITS = kKT * HD / 8;         // 16-byte units per K (or V) tile
-    constexpr int THREADS = 64 * G;
-    constexpr int UPT = UNITS / THREADS;        // units per thread per tile
-    constexpr int BLOCK_UNITS = 2 * HD;         // units per (block, kv head) tile
-    constexpr uint32_t kTile = kBS * HD;        // elements per (block, kv head) tile
-    static_assert(UNITS % THREADS == 0, "tile units must divide over the workgroup");
+    constexpr int HALVES = kQT / (kRG * R);  // workgroups per (item, KV head)
+    using S = TileShape<HD, G * R>;
+    constexpr int KS = S::KS;
+    constexpr int DT = S::DT;
+    constexpr int UPT = S::UPT;
+    constexpr uint32_t kTile = kBS * HD;  // elements per (block, kv head) tile
 
-    __shared__ __align__(16) uint8_t lds[2][2][TILE_BYTES];  // [buffer][K|V]
+    __shared__ __align__(16) uint8_t lds[2 * S::BUF];
 
-    const uint32_t item = blockIdx.x % num_items;
-    const uint32_t kvh = blockIdx.x / num_items;
-    const uint32_t row_begin = work[4 * item];
-    const uint32_t nrows = work[4 * item + 1];
-    const uint32_t p_min = work[4 * item + 2];
+    const uint32_t kvh = blockIdx.x % kv_heads;
+    const uint32_t rest = blockIdx.x / kv_heads;
+    const uint32_t item = rest / HALVES;
+    const uint32_t wg_row0 = (rest % HALVES) * (kRG * R);  // first item row of the workgroup
+    const uint32_t item_rows = work[4 * item + 1];
+    if (wg_row0 >= item_rows) return;  // whole workgroup, before any barrier
+    const uint32_t row_begin = work[4 * item] + wg_row0;
+    const uint32_t nrows = min(item_rows - wg_row0, static_cast<uint32_t>(kRG * R));
+    const uint32_t p_min = work[4 * item + 2] + wg_row0;
     const uint32_t seq = work[4 * item + 3];
     const uint32_t p_max = p_min + nrows - 1;
     const uint32_t n_tiles = p_max / kKT + 1;
@@ -103,99 +152,107 @@ __global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2))) voi
     const uint32_t *table = tables + table_off[seq];
 
     const uint32_t tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t c = lane & 31;  // query row of this lane within the tile
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t head = wave % G;  // query head of the wave within the group
+    const uint32_t rg = wave / G;    // row group of the wave
+    const uint32_t c = lane & 31;    // query row of this lane within the row group
     const uint32_t gl = lane >> 5;
-    const uint32_t qhead = kvh * G + wave;
-    const bool row_ok = c < nrows;
-    const uint32_t p_row = p_min + c;
+    const uint32_t qhead = kvh * G + head;
+    const uint32_t lr = kRG * rg + c;  // row within the workgroup
+    const bool row_ok = lr < nrows;
+    const uint32_t p_row = p_min + lr;
+    // Positions of the wave's first and last rows (wave-uniform).
+    const uint32_t wp_min = p_min + kRG * rg;
+    const uint32_t wp_max = min(wp_min + kRG - 1, p_max);
 
-    // Q^T operand, k-step kk: dims 16*kk + 8*gl .. +7 of row c.
+    // Q^T operand, k-step kk: dims 16*kk + 8*gl .. +7 of row lr.
     bf16x8 qv[KS];
     {
         const uint16_t *qp =
-            q + (static_cast<uint64_t>(row_begin + c) * num_heads + qhead) * HD + 8 * gl;
+            q + (static_cast<uint64_t>(row_begin + lr) * num_heads + qhead) * HD + 8 * gl;
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk)
             qv[kk] = row_ok ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 16 * kk))
                             : bf16x8{};
     }
 
-    // Global -> register staging of one KV tile, then register -> LDS.
+    // Lane b < 4 of the result holds the physical block of slot b of tile t.
+    auto load_table = [&](uint32_t t) -> uint32_t { return table[min(4 * t + (lane & 3), nblk - 1)]; };
+
+    // Global -> register staging of one KV tile.  K pair: lane = (key
+    // lane&15, 8-dim quarter lane>>4); V pair: lane = (dim lane&31, 8-key half
+    // lane>>5); both read 1 KiB that is contiguous in the pool.
+    const uint32_t k_lane = (lane & 15) * 32 + (lane >> 4) * 8;
+    const uint32_t v_lane = (lane & 31) * kBS + (lane >> 5) * 8;
     u32x4 kreg[UPT], vreg[UPT];
-    auto gload = [&](uint32_t t) {
+    auto gload = [&](uint32_t tbv) {
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-            const uint32_t U = tid + THREADS * i;
-            const uint32_t b = U / BLOCK_UNITS;
-            const uint32_t o = U % BLOCK_UNITS;
-            const uint32_t blk = table[min(4 * t + b, nblk - 1)];
-            const uint64_t base = (static_cast<uint64_t>(blk) * kv_heads + kvh) * kTile + 8 * o;
-            kreg[i] = *reinterpret_cast<const u32x4 *>(k_pool + base);
-            vreg[i] = *reinterpret_cast<const u32x4 *>(v_pool + base);
+            uint32_t b, ch;
+            S::pair(wave, i, b, ch);
+            const uint32_t blk = __builtin_amdgcn_readlane(tbv, b);
+            const uint64_t base = (static_cast<uint64_t>(blk) * kv_heads + kvh) * kTile + ch * (kBS * 32);
+            kreg[i] = *reinterpret_cast<const u32x4 *>(k_pool + base + k_lane);
+            vreg[i] = *reinterpret_cast<const u32x4 *>(v_pool + base + v_lane);
         }
     };
-    auto lstore = [&](int buf) {
-        uint8_t *kl = lds[buf][0];
-        uint8_t *vl = lds[buf][1];
+    // Register -> LDS: K row 16b + key at byte 64*ch + 16*quarter; V^T row
+    // 32*ch + dim at byte 32*b + 16*half.
+    const uint32_t k_st = (lane & 15) * S::KSTR + (lane >> 4) * 16;
+    const uint32_t v_st = S::KBYTES + (lane & 31) * S::VSTR + (lane >> 5) * 16;
+    auto lstore = [&](uint8_t *base) {
 #pragma unroll
         for (int i = 0; i < UPT; ++i) {
-            const uint32_t U = tid + THREADS * i;
-            const uint32_t b = U / BLOCK_UNITS;
-            const uint32_t o = U % BLOCK_UNITS;
-            // K pool tile [HD/32][16 keys][32 dims]: unit o = (chunk, key, quarter).
-            const uint32_t key = kBS * b + (o / 4) % kBS;
-            const uint32_t ku = (o / 64) * 4 + o % 4;
-            *reinterpret_cast<u32x4 *>(kl + key * KROW + swizzle<KUPR>(ku, key) * 16) = kreg[i];
-            // V pool tile [HD dims][16 keys]: unit o = (dim, half).
-            const uint32_t d = o / 2;
-            const uint32_t vu = 2 * b + o % 2;
-            *reinterpret_cast<u32x4 *>(vl + d * (kKT * 2) + swizzle<8>(vu, d) * 16) = vreg[i];
+            uint32_t b, ch;
+            S::pair(wave, i, b, ch);
+            *reinterpret_cast<u32x4 *>(base + k_st + (kBS * b) * S::KSTR + 64 * ch) = kreg[i];
+            *reinterpret_cast<u32x4 *>(base + v_st + (32 * ch) * S::VSTR + 32 * b) = vreg[i];
         }
     };
 
-    float m_run = -INFINITY;
+    float m_run = 0.0f;  // set by tile 0
     float l_run = 0.0f;
     floatx16 o_acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
 
-    const uint32_t ka = key_perm(c);  // A-row c of the Q.K^T MFMA reads key ka (+32)
+    // Per-lane LDS read offsets: K A-row c reads key key_perm(c) (+32),
+    // 16-byte unit 2*kk + gl; V^T A-row c reads dim 32*dt + c, unit 2*j + gl.
+    const uint32_t k_rd = key_perm(c) * S::KSTR + gl * 16;
+    const uint32_t v_rd = S::KBYTES + c * S::VSTR + gl * 16;
 
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
-    for (uint32_t t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
+    auto step = [&](auto buf_c, auto first_c, uint32_t t, uint32_t &tbv) {
+        constexpr int buf = decltype(buf_c)::value;
+        constexpr bool first = decltype(first_c)::value;
         const bool more = t + 1 < n_tiles;
-        if (more) gload(t + 1);
-
-        const uint8_t *kl = lds[buf][0];
-        const uint8_t *vl = lds[buf][1];
-
+        if (more) {
+            gload(tbv);
+            tbv = load_table(t + 2);
+        }
+        const uint8_t *tile = lds + buf * S::BUF;
+        const uint32_t j0 = t * kKT;
+        // A row group that ends before this tile (the workgroup's other row
+        // group reaches further) has nothing to add.
+        if (wp_min >= nrows + p_min || j0 > wp_max) goto staged;
+        {
         // S^T = K . Q^T for the two 32-key halves.
         floatx16 s0 = {}, s1 = {};
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
-            const uint32_t u = 2 * kk + gl;
-            const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(kl + ka * KROW + swizzle<KUPR>(u, ka) * 16);
-            const bf16x8 a1 =
-                *reinterpret_cast<const bf16x8 *>(kl + (32 + ka) * KROW + swizzle<KUPR>(u, 32 + ka) * 16);
+            const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(tile + k_rd + 32 * kk);
+            const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(tile + k_rd + 32 * S::KSTR + 32 * kk);
             s0 = mfma32x32x16(a0, qv[kk], s0);
             s1 = mfma32x32x16(a1, qv[kk], s1);
         }
 
-        // Online softmax for this lane's query row.
         float sc[32];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            sc[r] = s0[r] * scale_log2;
-            sc[16 + r] = s1[r] * scale_log2;
+            sc[r] = s0[r];
+            sc[16 + r] = s1[r];
         }
-        const uint32_t j0 = t * kKT;
-        if (j0 + kKT - 1 > p_min) {
+        if (j0 + kKT - 1 > wp_min) {
             // Diagonal tile: key j is visible to this row iff j <= p_row.
 #pragma unroll
             for (int r = 0; r < 32; ++r) {
@@ -203,25 +260,26 @@ __global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2))) voi
                 sc[r] = (key <= p_row) ? sc[r] : -INFINITY;
             }
         }
-        float mt = sc[0];
+        float mx = sc[0];
 #pragma unroll
-        for (int r = 1; r < 32; ++r) mt = fmaxf(mt, sc[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float m_new = fmaxf(m_run, mt);  // finite: tile 0 holds key 0 for every row
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        float ps = 0.0f;
+        for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mt = mx * scale_log2;  // finite: tile 0 holds key 0 for every row
+        if constexpr (first) {
+            m_run = mt;
+        } else if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazyLog2) != 0) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
 #pragma unroll
-        for (int r = 0; r < 32; ++r) {
-            sc[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
-            ps += sc[r];
+            for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
+            m_run = m_new;
         }
-        l_run = l_run * alpha + ps;
-        m_run = m_new;
+        const float nm = -m_run;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
+        for (int r = 0; r < 32; ++r) sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, nm));
 
         // O^T += V^T . P^T over four 16-key steps.
-        const bool split_p = (t == 0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             bf16x8 pb_hi, pb_lo;
@@ -230,27 +288,47 @@ __global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2))) voi
                 const float p = sc[16 * (j >> 1) + 8 * (j & 1) + i];
                 const __bf16 hi = static_cast<__bf16>(p);
                 pb_hi[i] = hi;
-                pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+                if constexpr (first) {
+                    pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+                    l_run += p;
+                }
             }
-            const uint32_t vu = 2 * j + gl;
+            if constexpr (!first) l_run = sum8(pb_hi, l_run);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const uint32_t d = 32 * dt + c;
-                const bf16x8 a =
-                    *reinterpret_cast<const bf16x8 *>(vl + d * (kKT * 2) + swizzle<8>(vu, d) * 16);
-                if (split_p) o_acc[dt] = mfma32x32x16(a, pb_lo, o_acc[dt]);
+                const bf16x8 a = *reinterpret_cast<const bf16x8 *>(tile + v_rd + 32 * dt * S::VSTR + 32 * j);
+                if constexpr (first) o_acc[dt] = mfma32x32x16(a, pb_lo, o_acc[dt]);
                 o_acc[dt] = mfma32x32x16(a, pb_hi, o_acc[dt]);
             }
         }
 
-        if (more) lstore(buf ^ 1);
+        }
+    staged:
+        if (more) lstore(lds + (buf ^ 1) * S::BUF);
         __syncthreads();
+    };
+
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using First = std::integral_constant<bool, true>;
+    using Rest = std::integral_constant<bool, false>;
+
+    uint32_t tbv = load_table(0);
+    gload(tbv);
+    tbv = load_table(1);
+    lstore(lds);
+    __syncthreads();
+    step(B0{}, First{}, 0, tbv);
+    for (uint32_t t = 1; t < n_tiles; t += 2) {
+        step(B1{}, Rest{}, t, tbv);
+        if (t + 1 >= n_tiles) break;
+        step(B0{}, Rest{}, t + 1, tbv);
     }
 
     l_run += __shfl_xor(l_run, 32, 64);
     if (!row_ok) return;
     const float inv = 1.0f / l_run;
-    uint16_t *op = out + (static_cast<uint64_t>(row_begin + c) * num_heads + qhead) * HD + 4 * gl;
+    uint16_t *op = out + (static_cast<uint64_t>(row_begin + lr) * num_heads + qhead) * HD + 4 * gl;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -269,12 +347,15 @@ template <int HD, int G>
 hipError_t launch_g(const PoolLayer &pool, const MetaView &meta, const PrefillPlan &plan,
                     const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
                     hipStream_t stream) {
-    const uint64_t grid = static_cast<uint64_t>(plan.num_items) * pool.kv_heads;
+    // Eight waves per workgroup: two row groups for up to 4 heads, one for 8.
+    constexpr int R = G <= 4 ? 2 : 1;
+    constexpr int HALVES = kQT / (kRG * R);
+    const uint64_t grid = static_cast<uint64_t>(plan.num_items) * HALVES * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("prefill_mfma", stream);
-    hipLaunchKernelGGL((prefill_mfma_kernel<HD, G>), dim3(static_cast<uint32_t>(grid)),
-                       dim3(64 * G), 0, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
-                       meta.tables, plan.work, plan.num_items, q, out, num_heads, scale_log2);
+    hipLaunchKernelGGL((prefill_mfma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
+                       dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
+                       meta.tables, plan.work, q, out, num_heads, scale_log2);
     return hipGetLastError();
 }
 
