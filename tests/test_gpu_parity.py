@@ -184,8 +184,8 @@ def test_decode_mfma_many_short_rows(vo, gpu_backend, hd):
 
 
 @pytest.mark.parametrize("split,waves", [("32", "1"), ("64", "2"), ("96", "4"), ("512", "1"),
-                                         ("512", "2"), ("2048", "4"), ("4096", "4"), ("32", "4"),
-                                         ("768", "8"), ("4096", "8")])
+                                         ("512", "2"), ("512", "4"), ("1024", "4"), ("2048", "4"),
+                                         ("4096", "4"), ("32", "4"), ("768", "8"), ("4096", "8")])
 def test_decode_mfma_split_and_wave_variants(vo, monkeypatch, split, waves):
     """Every split size and wavefront count gives the same results within
     tolerance, and a repeated call is bitwise identical."""
@@ -201,6 +201,32 @@ def test_decode_mfma_split_and_wave_variants(vo, monkeypatch, split, waves):
     _assert_close(out.float().cpu().numpy(), want, f"decode split={split} waves={waves}")
     again = _out(wl, backend)
     assert np.array_equal(_bits(again), _bits(out))
+
+
+def test_decode_streaming_loads_bitwise_equal(vo, monkeypatch):
+    """The non-temporal (streaming) and cached K/V load variants of the decode
+    kernel differ only in cache policy: the outputs are bitwise equal, on
+    disjoint tables (where the planner picks streaming) and on aliased ones
+    (where it picks cached loads)."""
+    _say("decode streaming vs cached loads")
+    backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=8192,
+                            max_query_heads=32)
+    for shared in (0, 640):
+        ctx = [shared + c for c in EDGE_CTX]
+        wl = W.build(vo, backend, kind="decode", heads=32, kv_heads=8, head_dim=128,
+                     block_size=16, num_blocks=3000, context_lens=ctx, seed=77,
+                     shared_prefix=shared, shared_count=len(ctx) if shared else 0)
+        outs = []
+        for nt in ("0", "1"):
+            monkeypatch.setenv("VO_DECODE_NT", nt)
+            outs.append(_bits(_out(wl, backend)))
+        monkeypatch.delenv("VO_DECODE_NT")
+        auto = _bits(_out(wl, backend))
+        assert np.array_equal(outs[0], outs[1]), f"shared={shared}"
+        assert np.array_equal(auto, outs[0]), f"shared={shared}"
+        want = W.oracle_attention(orc, wl)
+        got = backend.decode_attention(wl.q, wl.pool, 0, wl.meta).float().cpu().numpy()
+        _assert_close(got, want, f"streaming shared={shared}")
 
 
 def test_decode_cfg2_full_size(vo, gpu_backend):

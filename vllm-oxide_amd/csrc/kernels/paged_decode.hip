@@ -74,6 +74,19 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
 }
 
+// K/V tile load.  NT = non-temporal (streaming) loads: on MI355X they raise
+// random 4 KiB-tile read bandwidth from ~5.7 to ~6.4 TB/s; used when no KV
+// block is read by more than one row of the step, so nothing is lost by not
+// keeping the lines in L2.
+template <bool NT>
+__device__ __forceinline__ bf16x8 load_kv(const uint16_t *p) {
+    const u32x4 *v = reinterpret_cast<const u32x4 *>(p);
+    if constexpr (NT)
+        return __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(v));
+    else
+        return __builtin_bit_cast(bf16x8, *v);
+}
+
 // One chunk's K and V operands, in registers.
 template <int HD>
 struct Chunk {
@@ -91,7 +104,7 @@ struct LaneMap {
     bool v_hi;       // lane group g reads block b1 (g >= 2)
 };
 
-template <int HD>
+template <int HD, bool NT>
 __device__ __forceinline__ void load_chunk(Chunk<HD> &r, const uint16_t *k_head,
                                            const uint16_t *v_head, uint64_t block_stride,
                                            uint32_t phys0, uint32_t phys1, const LaneMap &lm) {
@@ -99,13 +112,13 @@ __device__ __forceinline__ void load_chunk(Chunk<HD> &r, const uint16_t *k_head,
         k_head + static_cast<uint64_t>(lm.k_hi ? phys1 : phys0) * block_stride + lm.k_off;
 #pragma unroll
     for (int kk = 0; kk < HD / 32; ++kk) {
-        r.ka[kk] = load_bf16x8(kp + kk * (kBS * 32));
-        r.kb[kk] = load_bf16x8(kp + 4 * 32 + kk * (kBS * 32));
+        r.ka[kk] = load_kv<NT>(kp + kk * (kBS * 32));
+        r.kb[kk] = load_kv<NT>(kp + 4 * 32 + kk * (kBS * 32));
     }
     const uint16_t *vp =
         v_head + static_cast<uint64_t>(lm.v_hi ? phys1 : phys0) * block_stride + lm.v_off;
 #pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt) r.va[dt] = load_bf16x8(vp + dt * 16 * kBS);
+    for (int dt = 0; dt < HD / 16; ++dt) r.va[dt] = load_kv<NT>(vp + dt * 16 * kBS);
 }
 
 // Online-softmax update with one chunk.  `nv` = valid keys of this lane's
@@ -170,7 +183,7 @@ __device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 *qv, bo
     }
 }
 
-template <int HD, int W>
+template <int HD, int W, bool NT>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void
 decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
                      uint32_t kv_heads, const uint32_t *__restrict__ table_off,
@@ -266,7 +279,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     auto load = [&](Chunk<HD> &r, uint32_t cc) {
         uint32_t p0, p1;
         phys(cc, p0, p1);
-        load_chunk<HD>(r, k_head, v_head, block_stride, p0, p1, lm);
+        load_chunk<HD, NT>(r, k_head, v_head, block_stride, p0, p1, lm);
     };
     uint32_t c = wave;
     if (c < nchunks) {
@@ -366,51 +379,76 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     }
 }
 
-// Merge the split-K partials of one (row, KV head) for the G query heads of
-// its group; rows with one split were written by the split kernel.  Each
-// thread owns 4 consecutive dims of one head and folds the splits in with a
-// running max, so all of its loads are independent of each other.
+// Merge the split-K partials of one (row, query head); rows with one split
+// were written by the split kernel.  The 256 threads are HD/4 dim quads x P
+// split lanes: lane p folds splits p, p + P, ... with a running max (its
+// loads are independent of each other), and the P lane results are merged
+// through LDS in lane order.  The merge order depends only on the row's
+// number of splits, so the result is the same in any batch.  With P lanes a
+// 64-split row costs 8 dependent load rounds instead of 64.
 template <int HD>
-__global__ __launch_bounds__(128) void decode_reduce_kernel(
+__global__ __launch_bounds__(256) void decode_reduce_kernel(
     const uint32_t *__restrict__ row_info, const float *__restrict__ part_acc,
-    const float *__restrict__ part_ml, uint16_t *__restrict__ out, uint32_t num_heads,
-    uint32_t kv_heads, uint32_t group) {
-    const uint32_t row = blockIdx.x / kv_heads;
-    const uint32_t kvh = blockIdx.x % kv_heads;
+    const float *__restrict__ part_ml, uint16_t *__restrict__ out, uint32_t num_heads) {
+    constexpr int NQ = HD / 4;     // dim quads of one head
+    constexpr int P = 256 / NQ;    // split lanes
+    __shared__ float s_m[P][NQ];
+    __shared__ float s_l[P][NQ];
+    __shared__ floatx4 s_acc[P][NQ];
+
+    const uint32_t row = blockIdx.x / num_heads;
+    const uint32_t qh = blockIdx.x % num_heads;
     const uint32_t first = row_info[2 * row];
     const uint32_t nsplit = row_info[2 * row + 1];
     if (nsplit <= 1) return;
-    const uint64_t out_base = static_cast<uint64_t>(row) * num_heads * HD;
-    for (uint32_t idx = threadIdx.x; idx < group * (HD / 4); idx += 128) {
-        const uint32_t qh = kvh * group + idx / (HD / 4);
-        const uint32_t d = 4 * (idx % (HD / 4));
-        const uint64_t p0 = static_cast<uint64_t>(first) * num_heads + qh;
-        float mx = -INFINITY, den = 0.0f;
-        floatx4 num = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (uint32_t i = 0; i < nsplit; ++i) {
-            const uint64_t p = p0 + static_cast<uint64_t>(i) * num_heads;
-            const float m = part_ml[2 * p];
-            const float l = part_ml[2 * p + 1];
-            const floatx4 a = *reinterpret_cast<const floatx4 *>(part_acc + p * HD + d);
-            const float m_new = fmaxf(mx, m);
-            const float scale_old = __builtin_amdgcn_exp2f(mx - m_new);
-            const float e = __builtin_amdgcn_exp2f(m - m_new);
-            den = den * scale_old + e * l;
-            num = num * scale_old + a * e;
-            mx = m_new;
-        }
-        const float inv = 1.0f / den;
-        u32x2 packed;
-        packed[0] = f32_to_bf16_bits(num[0] * inv) |
-                    (static_cast<uint32_t>(f32_to_bf16_bits(num[1] * inv)) << 16);
-        packed[1] = f32_to_bf16_bits(num[2] * inv) |
-                    (static_cast<uint32_t>(f32_to_bf16_bits(num[3] * inv)) << 16);
-        *reinterpret_cast<u32x2 *>(out + out_base + static_cast<uint64_t>(qh) * HD + d) = packed;
+    const uint32_t dq = threadIdx.x % NQ;
+    const uint32_t p = threadIdx.x / NQ;
+    const uint32_t d = 4 * dq;
+
+    float mx = -INFINITY, den = 0.0f;
+    floatx4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+    for (uint32_t i = p; i < nsplit; i += P) {
+        const uint64_t part = static_cast<uint64_t>(first + i) * num_heads + qh;
+        const float m = part_ml[2 * part];  // finite: a split holds >= 1 key
+        const float l = part_ml[2 * part + 1];
+        const floatx4 a = *reinterpret_cast<const floatx4 *>(part_acc + part * HD + d);
+        const float m_new = fmaxf(mx, m);
+        const float scale_old = __builtin_amdgcn_exp2f(mx - m_new);
+        const float e = __builtin_amdgcn_exp2f(m - m_new);
+        den = den * scale_old + e * l;
+        num = num * scale_old + a * e;
+        mx = m_new;
     }
+    s_m[p][dq] = mx;
+    s_l[p][dq] = den;
+    s_acc[p][dq] = num;
+    __syncthreads();
+    if (p != 0) return;
+    float M = s_m[0][dq];
+#pragma unroll
+    for (int j = 1; j < P; ++j) M = fmaxf(M, s_m[j][dq]);
+    float L = 0.0f;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        const float mj = s_m[j][dq];
+        if (mj == -INFINITY) continue;  // lane j had no split
+        const float e = __builtin_amdgcn_exp2f(mj - M);
+        L += e * s_l[j][dq];
+        acc += s_acc[j][dq] * e;
+    }
+    const float inv = 1.0f / L;
+    u32x2 packed;
+    packed[0] = f32_to_bf16_bits(acc[0] * inv) |
+                (static_cast<uint32_t>(f32_to_bf16_bits(acc[1] * inv)) << 16);
+    packed[1] = f32_to_bf16_bits(acc[2] * inv) |
+                (static_cast<uint32_t>(f32_to_bf16_bits(acc[3] * inv)) << 16);
+    const uint64_t out_off = (static_cast<uint64_t>(row) * num_heads + qh) * HD + d;
+    *reinterpret_cast<u32x2 *>(out + out_off) = packed;
 }
 
-template <int HD, int W>
+template <int HD, int W, bool NT>
 hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const DecodePlan &plan,
                         const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
                         hipStream_t stream) {
@@ -419,7 +457,7 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
     const uint64_t grid = static_cast<uint64_t>(plan.num_work) * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
-    hipLaunchKernelGGL((decode_splitk_kernel<HD, W>), dim3(static_cast<uint32_t>(grid)),
+    hipLaunchKernelGGL((decode_splitk_kernel<HD, W, NT>), dim3(static_cast<uint32_t>(grid)),
                        dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
                        meta.tables, meta.row_seq, meta.row_num_keys, plan.work, plan.row_info,
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
@@ -432,19 +470,23 @@ hipError_t launch_hd(const PoolLayer &pool, const MetaView &meta, const DecodePl
                      const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
                      int waves, hipStream_t stream) {
     hipError_t err;
+    const bool nt = plan.streaming;
+#define VO_SPLIT(Wv)                                                                            \
+    (nt ? launch_split<HD, Wv, true>(pool, meta, plan, q, out, num_heads, scale_log2, stream) \
+        : launch_split<HD, Wv, false>(pool, meta, plan, q, out, num_heads, scale_log2, stream))
     switch (waves) {
-        case 1: err = launch_split<HD, 1>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
-        case 2: err = launch_split<HD, 2>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
-        case 8: err = launch_split<HD, 8>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
-        default: err = launch_split<HD, 4>(pool, meta, plan, q, out, num_heads, scale_log2, stream); break;
+        case 1: err = VO_SPLIT(1); break;
+        case 2: err = VO_SPLIT(2); break;
+        case 8: err = VO_SPLIT(8); break;
+        default: err = VO_SPLIT(4); break;
     }
+#undef VO_SPLIT
     if (err != hipSuccess || !plan.needs_reduce) return err;
-    const uint64_t grid = static_cast<uint64_t>(meta.num_rows) * pool.kv_heads;
+    const uint64_t grid = static_cast<uint64_t>(meta.num_rows) * num_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_reduce", stream);
-    hipLaunchKernelGGL((decode_reduce_kernel<HD>), dim3(static_cast<uint32_t>(grid)), dim3(128),
-                       0, stream, plan.row_info, plan.part_acc, plan.part_ml, out, num_heads,
-                       pool.kv_heads, num_heads / pool.kv_heads);
+    hipLaunchKernelGGL((decode_reduce_kernel<HD>), dim3(static_cast<uint32_t>(grid)), dim3(256),
+                       0, stream, plan.row_info, plan.part_acc, plan.part_ml, out, num_heads);
     return hipGetLastError();
 }
 

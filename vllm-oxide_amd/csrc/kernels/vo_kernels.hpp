@@ -78,6 +78,7 @@ struct DecodePlan {
     float *part_acc;              // [parts][num_heads][head_dim]
     float *part_ml;               // [parts][num_heads][2]: (max, sum), log2 domain
     bool needs_reduce;            // some row has more than one split
+    bool streaming;               // no KV block is read by two rows: non-temporal K/V loads
 };
 
 // True when the MFMA decode kernel covers this shape.

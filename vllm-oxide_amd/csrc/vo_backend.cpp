@@ -142,6 +142,11 @@ namespace {
 enum MetaKind { kNone = 0, kPrefill = 1, kDecode = 2, kSlots = 3 };
 }
 
+// A row's last, shorter split in the decode work order (keys < split size).
+struct TailItem {
+    uint32_t keys, row, split;
+};
+
 struct vo_step_meta {
     int device = 0;
     int num_cus = 256;
@@ -180,6 +185,8 @@ struct vo_step_meta {
     const uint32_t *d_write_slots = nullptr;  // slots with superseded rows = kSkipSlot
     kernels::DecodePlan plan{};
     bool decode_planned = false;
+    std::vector<TailItem> tail_items;  // scratch of plan_decode (capacity kept across steps)
+    std::vector<uint8_t> block_seen;   // scratch of plan_decode: one byte per physical block
     kernels::PrefillPlan prefill_plan{};
     bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
 };
@@ -350,13 +357,35 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
 // order, and how the partials merge -- is the same alone or in any batch:
 // the reference's batch-invariance invariant (CLAUDE.md "Batch invariance",
 // model.rs:539-584).  VO_DECODE_SPLIT overrides L (a tuning knob).
-constexpr uint64_t kDefaultSplit = 512;
+constexpr uint64_t kDefaultSplit = 1024;
 
 uint64_t decode_split_keys() {
     const int env = env_int("VO_DECODE_SPLIT", 0);
     return (env >= 32 && env % 32 == 0 && env <= static_cast<int>(kernels::kMaxSplitKeys))
                ? static_cast<uint64_t>(env)
                : kDefaultSplit;
+}
+
+// True when no physical block is read by two rows of this decode step (no
+// prefix sharing through aliased table entries): the decode kernel then
+// streams K/V with non-temporal loads.  When blocks are shared, the cached
+// loads let later rows hit the shared prefix in L2 / MALL.  Either way the
+// arithmetic is identical.  VO_DECODE_NT=0/1 forces the choice.
+bool decode_streaming(vo_step_meta *m) {
+    const int env = env_int("VO_DECODE_NT", -1);
+    if (env == 0 || env == 1) return env == 1;
+    const uint64_t bs = m->block_size;
+    m->block_seen.assign(static_cast<size_t>(m->max_block) + 1, 0);
+    for (uint64_t r = 0; r < m->num_rows; ++r) {
+        const uint64_t seq = m->row_seq[r];
+        const uint64_t used = (m->row_num_keys[r] + bs - 1) / bs;
+        const uint32_t *t = m->tables.data() + m->table_off[seq];
+        for (uint64_t i = 0; i < used; ++i) {
+            if (m->block_seen[t[i]]) return false;
+            m->block_seen[t[i]] = 1;
+        }
+    }
+    return true;
 }
 
 // Rows with zero keys still get one work item (it writes the zero output).
@@ -375,20 +404,44 @@ vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
     m->plan.work = dp;
     uint32_t *row_info = pk.add(2 * T, &dp);
     m->plan.row_info = dp;
+    // Work order, longest first: every full split (L keys) in row order, then
+    // each row's shorter last split by descending length.  The hardware deals
+    // workgroups out in grid order as slots free up, so the short items fill
+    // the gaps at the end instead of a full split starting last and running
+    // alone.  Partials are addressed by (row, split), so the order changes no
+    // arithmetic.
     uint64_t n = 0;
     bool needs_reduce = false;
     for (uint64_t r = 0; r < T; ++r) {
-        const uint64_t ns = row_splits(m->row_num_keys[r], L);
+        const uint64_t nk = m->row_num_keys[r];
+        const uint64_t ns = row_splits(nk, L);
         row_info[2 * r] = static_cast<uint32_t>(n);
         row_info[2 * r + 1] = static_cast<uint32_t>(ns);
+        n += ns;
         if (ns > 1) needs_reduce = true;
-        for (uint64_t s = 0; s < ns; ++s, ++n) {
-            work[2 * n] = static_cast<uint32_t>(r);
-            work[2 * n + 1] = static_cast<uint32_t>(s);
+    }
+    m->tail_items.clear();
+    uint64_t f = 0;
+    for (uint64_t r = 0; r < T; ++r) {
+        const uint64_t nk = m->row_num_keys[r];
+        for (uint64_t s = 0; s < nk / L; ++s, ++f) {
+            work[2 * f] = static_cast<uint32_t>(r);
+            work[2 * f + 1] = static_cast<uint32_t>(s);
         }
+        if (nk % L != 0 || nk == 0)
+            m->tail_items.push_back({static_cast<uint32_t>(nk % L), static_cast<uint32_t>(r),
+                                     static_cast<uint32_t>(nk / L)});
+    }
+    std::stable_sort(m->tail_items.begin(), m->tail_items.end(),
+                     [](const TailItem &a, const TailItem &b) { return a.keys > b.keys; });
+    for (const TailItem &t : m->tail_items) {
+        work[2 * f] = t.row;
+        work[2 * f + 1] = t.split;
+        ++f;
     }
     m->plan.num_work = static_cast<uint32_t>(parts);
     m->plan.split_keys = static_cast<uint32_t>(L);
+    m->plan.streaming = decode_streaming(m);
     m->plan.part_acc = m->d_part_acc;
     m->plan.part_ml = m->d_part_ml;
     m->plan.needs_reduce = needs_reduce;
