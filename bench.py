@@ -252,13 +252,54 @@ def bench_prefill(vo, W, orc, args):
     }
 
 
+def bench_mixed(vo, W, orc, args):
+    """BASELINE config 4's attention step: 256 decode sequences (lognormal
+    context, median 1024) + two 512-row chunks in one write_kv +
+    prefill_attention call (the decode rows run on the split-K kernel, the
+    chunks on the MFMA prefill kernel)."""
+    import torch
+    heads, kvh, hd, bs = 32, 8, 128, 16
+    ctx, new = W.cfg4_attention_lens()
+    backend = vo.HipBackend(device=0, max_seqs=len(ctx), max_rows=W.FILL_ROWS,
+                            max_table_entries=30000, max_query_heads=heads)
+    wl = W.build(vo, backend, kind="prefill", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=bs, num_blocks=30000, context_lens=ctx, num_new=new, seed=4,
+                 num_layers=args.layers, fill_layers=list(range(args.layers)), keep_host=False)
+    out = torch.empty_like(wl.q)
+
+    def step(i):
+        layer = i % args.layers
+        backend.write_kv(wl.pool, layer, wl.k_new, wl.v_new, wl.meta)
+        backend.prefill_attention(wl.q, wl.pool, layer, wl.meta, out=out)
+
+    sec = time_steps(torch, step, args.steps, args.warmup)
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    time_steps(torch, step, args.steps, 0)
+    vo.enable_profiling(False)
+    prof = vo.profile()
+    dec = int((np.asarray(new) == 1).sum())
+    return {
+        "metric": "mixed continuous-batching attention step (cfg4 shape), 1 GPU",
+        "value": round(wl.rows / sec, 1), "unit": "tokens/s", "n_gpus": 1,
+        "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg4 attention: 256 decode (lognormal median 1024, sigma 1, "
+                               "clip [128, 8192], seed 4) + 2 x 512-row chunks (ctx 0, 1536)",
+                   "step": "write_kv + prefill_attention (one call, mixed rows)",
+                   "decode_row_routing": os.environ.get("VO_PREFILL_DECODE_ROWS", "1") != "0"},
+        "decode_tokens_per_s": round(dec / sec, 1),
+        "kernels_us": {k: round(v["avg_ms"] * 1e3, 2) for k, v in prof.items()},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=2, help="pool layers to rotate over")
-    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg5", "all"])
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg5", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
@@ -306,6 +347,8 @@ def main():
         lines.append(bench_decode(vo, W, orc, args, cfg))
     if args.config in ("cfg3", "all"):
         lines.append(bench_prefill(vo, W, orc, args))
+    if args.config in ("cfg4a", "all"):
+        lines.append(bench_mixed(vo, W, orc, args))
     for line in lines:
         print(json.dumps(line), flush=True)
 

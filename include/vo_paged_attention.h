@@ -148,6 +148,27 @@ int32_t vo_decode_meta_build(const vo_decode_seq *seqs, uint64_t num_seqs,
                              uint32_t *slot_mapping, uint64_t *row_seq,
                              uint64_t *row_num_keys);
 
+/* PrefillMeta::new (paged.rs:117-143) on the device.  No counterpart in the
+ * reference, which builds a step's metadata on the host: this is for callers
+ * that keep a batch's per-sequence state in device memory (context lengths,
+ * CSR block tables) and want the per-row arrays without a host round trip.
+ * Inputs, all device u32 arrays: seq_row_starts [S+1] (row offsets, from 0
+ * to num_rows), context_lens [S], table_off [S+1], tables [table_off[S]].
+ * Outputs, device u32 arrays [num_rows]: positions, slot_mapping, row_seq,
+ * row_num_keys, exactly the values vo_prefill_meta_build returns.  A decode
+ * step (DecodeMeta::new, paged.rs:189-209) is seq_row_starts[s] = s.
+ * The coverage check of paged.rs:64-80 runs on the device: a row whose
+ * position lies past its sequence's table gets slot 0xffffffff and sets
+ * *errors (a device u32 the call does not clear) to 1, so the caller checks
+ * the flag where the reference would return BlockTableTooShort.
+ * Asynchronous on `stream`; the caller keeps the arrays alive until it ends. */
+int32_t vo_prefill_meta_build_device(const uint32_t *seq_row_starts, const uint32_t *context_lens,
+                                     const uint32_t *table_off, const uint32_t *tables,
+                                     uint64_t num_seqs, uint64_t num_rows, uint64_t block_size,
+                                     uint32_t *positions, uint32_t *slot_mapping,
+                                     uint32_t *row_seq, uint32_t *row_num_keys, uint32_t *errors,
+                                     void *stream);
+
 /* PrefillMeta::last_rows (paged.rs:154-159): out[s] = seq_row_starts[s+1]-1. */
 int32_t vo_last_rows(const uint64_t *seq_row_starts, uint64_t num_seqs, uint32_t *out);
 

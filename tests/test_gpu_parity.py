@@ -326,6 +326,75 @@ def test_prefill_cfg3_full_size_sampled_rows(vo, gpu_backend):
     _assert_close(out[rows], want, "cfg3")
 
 
+MIXED_CTX = [0, 1, 15, 16, 17, 63, 64, 65, 700, 1023, 1024, 1025, 3000, 0, 100, 700, 5, 2047]
+MIXED_NEW = [1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 100, 200, 2, 33]
+
+
+def test_mixed_step_matches_oracle(vo, gpu_backend):
+    """One prefill_attention call carrying decode sequences (one new row, run
+    on the split-K decode kernel) and chunks (run on the MFMA prefill
+    kernel), as a continuous-batching step does (model.rs:312-319)."""
+    _say("mixed step vs oracle")
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=1500, context_lens=MIXED_CTX, num_new=MIXED_NEW,
+                 seed=41)
+    out = _out(wl, gpu_backend)
+    want = W.oracle_attention(orc, wl)
+    _assert_close(out.float().cpu().numpy(), want, "mixed step")
+
+
+def test_mixed_step_decode_rows_bitwise_equal_decode_call(vo, gpu_backend):
+    """A sequence with one new row gets, inside a mixed prefill call, bitwise
+    the output decode_attention gives it: its arithmetic does not depend on
+    the rest of the batch (CLAUDE.md batch invariance, model.rs:539-584)."""
+    import torch
+    _say("mixed step decode rows == decode call")
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=1500, context_lens=MIXED_CTX, num_new=MIXED_NEW,
+                 seed=42)
+    mixed = _bits(_out(wl, gpu_backend))
+    starts = np.asarray(wl.meta.seq_row_starts, dtype=np.int64)
+    dec_seqs = [s for s in range(len(MIXED_CTX)) if MIXED_NEW[s] == 1]
+    rows = [int(starts[s]) for s in dec_seqs]
+    meta = vo.DecodeMeta.new([vo.DecodeSeq(MIXED_CTX[s], wl.tables[s]) for s in dec_seqs], 16)
+    q = wl.q[torch.tensor(rows, device=wl.q.device)].contiguous()
+    dec = _bits(gpu_backend.decode_attention(q, wl.pool, 0, meta))
+    assert np.array_equal(dec, mixed[rows])
+
+
+def test_mixed_step_routing_off_matches_oracle(vo, monkeypatch):
+    """With the decode-row routing switched off (VO_PREFILL_DECODE_ROWS=0)
+    every row runs on the prefill kernel; results agree within tolerance."""
+    monkeypatch.setenv("VO_PREFILL_DECODE_ROWS", "0")
+    _say("mixed step, routing off")
+    backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=4096,
+                            max_query_heads=32)
+    wl = W.build(vo, backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=1500, context_lens=MIXED_CTX, num_new=MIXED_NEW,
+                 seed=43)
+    out = _out(wl, backend)
+    want = W.oracle_attention(orc, wl)
+    _assert_close(out.float().cpu().numpy(), want, "mixed step, routing off")
+
+
+def test_mixed_step_cfg4_attention_full_size(vo):
+    """BASELINE config 4's attention shape: 256 decode sequences (lognormal
+    context, median 1024) + two 512-row chunks in one prefill_attention call;
+    every row on the GPU, a sample of rows by the oracle."""
+    _say("mixed step cfg4 attention shape")
+    ctx, new = W.cfg4_attention_lens()
+    backend = vo.HipBackend(device=0, max_seqs=300, max_rows=W.FILL_ROWS,
+                            max_table_entries=30000, max_query_heads=32)
+    wl = W.build(vo, backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=30000, context_lens=ctx, num_new=new, seed=4)
+    out = _out(wl, backend).float().cpu().numpy()
+    starts = np.asarray(wl.meta.seq_row_starts, dtype=np.int64)
+    rows = np.unique(np.concatenate([np.arange(0, 256, 5), np.arange(256, wl.rows, 37),
+                                     starts[-3:] - 1]))
+    want = W.oracle_attention(orc, wl, rows=rows)
+    _assert_close(out[rows], want, "cfg4 attention")
+
+
 def test_prefill_row_matches_decode_within_tolerance(vo, gpu_backend):
     """A prefill row at position p and a decode at context p see the same keys."""
     _say("prefill row vs decode")
@@ -368,3 +437,75 @@ def test_errors_match_reference_classes(vo, gpu_backend):
     with pytest.raises(vo.ShapeError):  # decode op given prefill metadata
         gpu_backend.decode_attention(q, pool, 0, pm)
     torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# Step metadata built on the device (PrefillMeta::new / DecodeMeta::new)
+# ---------------------------------------------------------------------------
+def _device_rows(vo, seq_row_starts, context_lens, tables, block_size):
+    import torch
+    off = np.concatenate([[0], np.cumsum([len(t) for t in tables])]).astype(np.int64)
+    flat = np.concatenate([np.asarray(t, np.uint32) for t in tables] + [np.zeros(1, np.uint32)])
+    d = lambda a: torch.tensor(np.asarray(a, np.int64).astype(np.uint32).view(np.int32),
+                               device="cuda:0")
+    T = int(seq_row_starts[-1])
+    pos, slot, rseq, rkeys, err = vo.prefill_meta_build_device(
+        d(seq_row_starts), d(context_lens), d(off), d(flat), block_size, T)
+    torch.cuda.synchronize()
+    u = lambda t: t.cpu().numpy().view(np.uint32)
+    return u(pos), u(slot), u(rseq), u(rkeys), int(err.cpu()[0])
+
+
+def test_device_meta_reference_kats(vo):
+    """paged.rs:230-285 known answers, built on the device."""
+    _say("device meta KATs")
+    pos, slot, rseq, rkeys, err = _device_rows(vo, [0, 5, 8], [0, 6], [[3, 0], [1, 4, 6]], 4)
+    assert err == 0
+    assert list(pos) == [0, 1, 2, 3, 4, 6, 7, 8]
+    assert list(slot) == [12, 13, 14, 15, 0, 18, 19, 24]
+    assert list(rseq) == [0, 0, 0, 0, 0, 1, 1, 1]
+    assert list(rkeys) == [1, 2, 3, 4, 5, 7, 8, 9]
+    pos, slot, rseq, rkeys, err = _device_rows(vo, [0, 1, 2], [0, 6], [[9], [2, 5]], 4)
+    assert err == 0
+    assert list(pos) == [0, 6] and list(slot) == [36, 22]
+    assert list(rseq) == [0, 1] and list(rkeys) == [1, 7]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_device_meta_bit_exact_vs_oracle(vo, seed):
+    """Random batches (empty sequences, chunks ending on and off block
+    boundaries, decode-shaped steps): the device arrays equal the oracle's
+    PrefillMeta / DecodeMeta bit for bit."""
+    _say(f"device meta vs oracle seed={seed}")
+    rng = np.random.default_rng(seed)
+    for trial in range(20):
+        S = int(rng.integers(1, 40))
+        bs = int(rng.choice([1, 4, 16, 32]))
+        decode = trial % 4 == 0
+        ctx = rng.integers(0, 3000, S)
+        new = np.ones(S, np.int64) if decode else rng.integers(0, 300, S)
+        hi = (1 << 32) - 1 if trial % 5 == 1 else 1 << 20  # u32 slot arithmetic wraps
+        tables = [rng.integers(0, hi, -(-int(c + n) // bs) + int(rng.integers(0, 3)),
+                               dtype=np.uint64).astype(np.uint32) for c, n in zip(ctx, new)]
+        starts = np.concatenate([[0], np.cumsum(new)])
+        pos, slot, rseq, rkeys, err = _device_rows(vo, starts, ctx, tables, bs)
+        assert err == 0
+        if decode:
+            want = orc.decode_meta([(int(c), t) for c, t in zip(ctx, tables)], bs)
+        else:
+            want = orc.prefill_meta([(int(c), int(n), t) for c, n, t in zip(ctx, new, tables)],
+                                    bs)
+        assert np.array_equal(pos, np.asarray(want["positions"], np.uint32))
+        assert np.array_equal(slot, np.asarray(want["slot_mapping"], np.uint32))
+        assert np.array_equal(rseq, np.asarray(want["row_seq"], np.uint32))
+        assert np.array_equal(rkeys, np.asarray(want["row_num_keys"], np.uint32))
+
+
+def test_device_meta_flags_uncovered_rows(vo):
+    """paged.rs:287-318: 5 tokens on a one-block table of block size 4 are not
+    covered; the device build flags it and marks the uncovered row's slot."""
+    _say("device meta coverage flag")
+    pos, slot, rseq, rkeys, err = _device_rows(vo, [0, 5], [0], [[7]], 4)
+    assert err == 1
+    assert list(slot[:4]) == [28, 29, 30, 31] and slot[4] == 0xffffffff
+

@@ -213,6 +213,21 @@ def cfg3_context_lens(seed=3, num_seqs=8, hi=8192):
     return rng.integers(0, hi + 1, num_seqs)
 
 
+def cfg4_attention_lens(seed=4, num_decode=256, median=1024, sigma=1.0, lo=128, hi=8192,
+                        chunk_ctx=(0, 1536), chunk=512):
+    """The attention part of BASELINE config 4's mixed step: 256 decode
+    sequences with context lognormal (median 1024, sigma 1.0 -- BASELINE
+    leaves sigma open) clipped to [128, 8192], plus two 512-row prefill
+    chunks, one at the start of its prompt and one continuing a prompt whose
+    first 1536 tokens are cached.  Returns (context_lens, num_new)."""
+    rng = np.random.default_rng(seed)
+    dec = np.clip(np.round(np.exp(np.log(median) + sigma * rng.standard_normal(num_decode))),
+                  lo, hi).astype(np.int64)
+    ctx = np.concatenate([dec, np.asarray(chunk_ctx, np.int64)])
+    new = np.concatenate([np.ones(num_decode, np.int64), np.full(len(chunk_ctx), chunk, np.int64)])
+    return ctx, new
+
+
 def cfg5_context_lens(seed=5, num_seqs=64, prefix=4096, lo=256, hi=1024, long_ctx=32768):
     """64 sequences share a 4096-token prefix and add a
     suffix uniform in [256, 1024]; one more sequence at 32768 context."""

@@ -113,6 +113,8 @@ SIGNATURES = {
     "vo_prefill_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
     "vo_decode_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
     "vo_gather_kv": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _vp, _vp, _vp]),
+    "vo_prefill_meta_build_device": (ctypes.c_int32, [_vp, _vp, _vp, _vp, _u64, _u64, _u64,
+                                                      _vp, _vp, _vp, _vp, _vp, _vp]),
     "vo_profiling_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "vo_profile_read": (ctypes.c_int32, [ctypes.POINTER(vo_kernel_stat), _u64, _u64p]),
     "vo_profile_reset": (None, []),
@@ -574,3 +576,26 @@ class HipBackend:
         _check(lib.vo_gather_kv(pool.handle, layer, m.handle, seq, num_keys, _dev_ptr(k),
                                 _dev_ptr(v), _stream_ptr(stream)))
         return k[:num_keys], v[:num_keys]
+
+
+def prefill_meta_build_device(seq_row_starts, context_lens, table_off, tables, block_size: int,
+                              num_rows: int, stream=None):
+    """PrefillMeta::new (paged.rs:117-143) on the device from device ``torch.int32``
+    tensors (read as u32): seq_row_starts [S+1], context_lens [S], table_off [S+1],
+    tables [entries].  Returns (positions, slot_mapping, row_seq, row_num_keys, errors)
+    as device int32 tensors (u32 bit patterns); ``errors[0]`` is 1 when some row's
+    position lies past its table (the reference's BlockTableTooShort)."""
+    import torch
+    for t in (seq_row_starts, context_lens, table_off, tables):
+        if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.int32
+                and t.is_contiguous()):
+            raise TypeError("expected contiguous int32 device tensors")
+    dev = seq_row_starts.device
+    S = seq_row_starts.numel() - 1
+    outs = [torch.empty(max(num_rows, 1), dtype=torch.int32, device=dev) for _ in range(4)]
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    _check(lib.vo_prefill_meta_build_device(
+        _vp(seq_row_starts.data_ptr()), _vp(context_lens.data_ptr()), _vp(table_off.data_ptr()),
+        _vp(tables.data_ptr()), S, num_rows, block_size, *[_vp(o.data_ptr()) for o in outs],
+        _vp(err.data_ptr()), _stream_ptr(stream)))
+    return tuple(o[:num_rows] for o in outs) + (err,)

@@ -379,8 +379,9 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     }
 }
 
-// Merge the split-K partials of one (row, query head); rows with one split
-// were written by the split kernel.  The 256 threads are HD/4 dim quads x P
+// Merge the split-K partials of one (row, query head) for the rows listed in
+// reduce_rows (those with more than one split; rows with one split were
+// written by the split kernel).  The 256 threads are HD/4 dim quads x P
 // split lanes: lane p folds splits p, p + P, ... with a running max (its
 // loads are independent of each other), and the P lane results are merged
 // through LDS in lane order.  The merge order depends only on the row's
@@ -388,19 +389,19 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
 // 64-split row costs 8 dependent load rounds instead of 64.
 template <int HD>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
-    const uint32_t *__restrict__ row_info, const float *__restrict__ part_acc,
-    const float *__restrict__ part_ml, uint16_t *__restrict__ out, uint32_t num_heads) {
+    const uint32_t *__restrict__ row_info, const uint32_t *__restrict__ reduce_rows,
+    const float *__restrict__ part_acc, const float *__restrict__ part_ml,
+    uint16_t *__restrict__ out, uint32_t num_heads) {
     constexpr int NQ = HD / 4;     // dim quads of one head
     constexpr int P = 256 / NQ;    // split lanes
     __shared__ float s_m[P][NQ];
     __shared__ float s_l[P][NQ];
     __shared__ floatx4 s_acc[P][NQ];
 
-    const uint32_t row = blockIdx.x / num_heads;
+    const uint32_t row = reduce_rows[blockIdx.x / num_heads];
     const uint32_t qh = blockIdx.x % num_heads;
     const uint32_t first = row_info[2 * row];
     const uint32_t nsplit = row_info[2 * row + 1];
-    if (nsplit <= 1) return;
     const uint32_t dq = threadIdx.x % NQ;
     const uint32_t p = threadIdx.x / NQ;
     const uint32_t d = 4 * dq;
@@ -481,12 +482,13 @@ hipError_t launch_hd(const PoolLayer &pool, const MetaView &meta, const DecodePl
         default: err = VO_SPLIT(4); break;
     }
 #undef VO_SPLIT
-    if (err != hipSuccess || !plan.needs_reduce) return err;
-    const uint64_t grid = static_cast<uint64_t>(meta.num_rows) * num_heads;
+    if (err != hipSuccess || plan.num_reduce_rows == 0) return err;
+    const uint64_t grid = static_cast<uint64_t>(plan.num_reduce_rows) * num_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_reduce", stream);
     hipLaunchKernelGGL((decode_reduce_kernel<HD>), dim3(static_cast<uint32_t>(grid)), dim3(256),
-                       0, stream, plan.row_info, plan.part_acc, plan.part_ml, out, num_heads);
+                       0, stream, plan.row_info, plan.reduce_rows, plan.part_acc, plan.part_ml,
+                       out, num_heads);
     return hipGetLastError();
 }
 
@@ -500,7 +502,7 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               const DecodePlan &plan, const uint16_t *q, uint16_t *out,
                               uint32_t num_heads, float scale, int waves_per_group,
                               hipStream_t stream) {
-    if (meta.num_rows == 0 || plan.num_work == 0) return hipSuccess;
+    if (plan.num_work == 0) return hipSuccess;
     if (plan.split_keys == 0 || plan.split_keys % kChunk != 0 || plan.split_keys > kMaxSplitKeys)
         return hipErrorInvalidValue;
     const float scale_log2 = scale * 1.4426950408889634f;

@@ -66,18 +66,30 @@ hipError_t launch_attention_generic(const PoolLayer &pool, const MetaView &meta,
                                     const uint16_t *q, uint16_t *out, uint32_t num_heads,
                                     float scale, hipStream_t stream);
 
+// PrefillMeta::new / DecodeMeta::new on the device (paged.rs:117-143,
+// 189-209): per-row positions, slots, sequences and key counts from the
+// per-sequence row starts, context lengths and CSR block tables (all device
+// u32 arrays).  Uncovered positions get slot 0xffffffff and set *errors = 1.
+hipError_t launch_build_rows(const uint32_t *seq_row_starts, const uint32_t *context_lens,
+                             const uint32_t *table_off, const uint32_t *tables, uint32_t num_seqs,
+                             uint32_t num_rows, uint32_t block_size, uint32_t *positions,
+                             uint32_t *slot_mapping, uint32_t *row_seq, uint32_t *row_num_keys,
+                             uint32_t *errors, hipStream_t stream);
+
 // Largest split the decode kernel takes (its block-table slice lives in LDS).
 constexpr uint32_t kMaxSplitKeys = 4096;
 
 // Split-K work plan for the MFMA decode kernel.
 struct DecodePlan {
     const uint32_t *work;         // [num_work][2]: (row, split); a zero-key row has one item
-    const uint32_t *row_info;     // [T][2]: (first partial index, number of splits)
+    const uint32_t *row_info;     // [T][2]: (first partial index, number of splits); (0, 0) for
+                                  // rows the plan does not cover
+    const uint32_t *reduce_rows;  // [num_reduce_rows]: rows with more than one split
     uint32_t num_work;
+    uint32_t num_reduce_rows;
     uint32_t split_keys;          // keys per split, a multiple of 32, <= kMaxSplitKeys
     float *part_acc;              // [parts][num_heads][head_dim]
     float *part_ml;               // [parts][num_heads][2]: (max, sum), log2 domain
-    bool needs_reduce;            // some row has more than one split
     bool streaming;               // no KV block is read by two rows: non-temporal K/V loads
 };
 

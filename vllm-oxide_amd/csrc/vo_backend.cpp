@@ -187,6 +187,8 @@ struct vo_step_meta {
     bool decode_planned = false;
     std::vector<TailItem> tail_items;  // scratch of plan_decode (capacity kept across steps)
     std::vector<uint8_t> block_seen;   // scratch of plan_decode: one byte per physical block
+    std::vector<uint64_t> seq_keys;    // scratch of plan_decode: keys read per sequence
+    std::vector<uint32_t> decode_rows; // rows of a prefill step planned on the decode kernel
     kernels::PrefillPlan prefill_plan{};
     bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
 };
@@ -366,19 +368,23 @@ uint64_t decode_split_keys() {
                : kDefaultSplit;
 }
 
-// True when no physical block is read by two rows of this decode step (no
+// True when no physical block is read by two sequences of this step (no
 // prefix sharing through aliased table entries): the decode kernel then
 // streams K/V with non-temporal loads.  When blocks are shared, the cached
 // loads let later rows hit the shared prefix in L2 / MALL.  Either way the
-// arithmetic is identical.  VO_DECODE_NT=0/1 forces the choice.
+// arithmetic is identical.  Each sequence's used table prefix is checked
+// once (its last row has the most keys).  VO_DECODE_NT=0/1 forces the choice.
 bool decode_streaming(vo_step_meta *m) {
     const int env = env_int("VO_DECODE_NT", -1);
     if (env == 0 || env == 1) return env == 1;
     const uint64_t bs = m->block_size;
+    const uint64_t S = m->num_seqs;
+    m->seq_keys.assign(S, 0);
+    for (uint64_t r = 0; r < m->num_rows; ++r)
+        m->seq_keys[m->row_seq[r]] = std::max<uint64_t>(m->seq_keys[m->row_seq[r]], m->row_num_keys[r]);
     m->block_seen.assign(static_cast<size_t>(m->max_block) + 1, 0);
-    for (uint64_t r = 0; r < m->num_rows; ++r) {
-        const uint64_t seq = m->row_seq[r];
-        const uint64_t used = (m->row_num_keys[r] + bs - 1) / bs;
+    for (uint64_t seq = 0; seq < S; ++seq) {
+        const uint64_t used = (m->seq_keys[seq] + bs - 1) / bs;
         const uint32_t *t = m->tables.data() + m->table_off[seq];
         for (uint64_t i = 0; i < used; ++i) {
             if (m->block_seen[t[i]]) return false;
@@ -391,42 +397,48 @@ bool decode_streaming(vo_step_meta *m) {
 // Rows with zero keys still get one work item (it writes the zero output).
 uint64_t row_splits(uint64_t keys, uint64_t L) { return keys ? (keys + L - 1) / L : 1; }
 
-vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
+// Split-K plan over the rows listed in `rows` (every row of the step when
+// rows is null).  Rows outside the plan get row_info (0, 0).
+vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32_t> *rows) {
     const uint64_t T = m->num_rows;
     const uint64_t L = decode_split_keys();
+    const uint64_t R = rows ? rows->size() : T;
+    auto row_at = [&](uint64_t i) -> uint64_t { return rows ? (*rows)[i] : i; };
     uint64_t parts = 0;
-    for (uint64_t r = 0; r < T; ++r) parts += row_splits(m->row_num_keys[r], L);
+    for (uint64_t i = 0; i < R; ++i) parts += row_splits(m->row_num_keys[row_at(i)], L);
     if (parts > m->max_parts) return fail_capacity("split-K partials per step", parts, m->max_parts);
-    (void)op;
 
     const uint32_t *dp;
     uint32_t *work = pk.add(2 * parts, &dp);
     m->plan.work = dp;
     uint32_t *row_info = pk.add(2 * T, &dp);
     m->plan.row_info = dp;
+    uint32_t *reduce_rows = pk.add(R, &dp);
+    m->plan.reduce_rows = dp;
     // Work order, longest first: every full split (L keys) in row order, then
     // each row's shorter last split by descending length.  The hardware deals
     // workgroups out in grid order as slots free up, so the short items fill
     // the gaps at the end instead of a full split starting last and running
     // alone.  Partials are addressed by (row, split), so the order changes no
     // arithmetic.
-    uint64_t n = 0;
-    bool needs_reduce = false;
-    for (uint64_t r = 0; r < T; ++r) {
-        const uint64_t nk = m->row_num_keys[r];
-        const uint64_t ns = row_splits(nk, L);
+    if (rows) std::fill(row_info, row_info + 2 * T, 0u);
+    uint64_t n = 0, nred = 0;
+    for (uint64_t i = 0; i < R; ++i) {
+        const uint64_t r = row_at(i);
+        const uint64_t ns = row_splits(m->row_num_keys[r], L);
         row_info[2 * r] = static_cast<uint32_t>(n);
         row_info[2 * r + 1] = static_cast<uint32_t>(ns);
         n += ns;
-        if (ns > 1) needs_reduce = true;
+        if (ns > 1) reduce_rows[nred++] = static_cast<uint32_t>(r);
     }
     m->tail_items.clear();
     uint64_t f = 0;
-    for (uint64_t r = 0; r < T; ++r) {
+    for (uint64_t i = 0; i < R; ++i) {
+        const uint64_t r = row_at(i);
         const uint64_t nk = m->row_num_keys[r];
-        for (uint64_t s = 0; s < nk / L; ++s, ++f) {
+        for (uint64_t sp = 0; sp < nk / L; ++sp, ++f) {
             work[2 * f] = static_cast<uint32_t>(r);
-            work[2 * f + 1] = static_cast<uint32_t>(s);
+            work[2 * f + 1] = static_cast<uint32_t>(sp);
         }
         if (nk % L != 0 || nk == 0)
             m->tail_items.push_back({static_cast<uint32_t>(nk % L), static_cast<uint32_t>(r),
@@ -440,36 +452,52 @@ vo_status plan_decode(vo_step_meta *m, Packer &pk, const char *op) {
         ++f;
     }
     m->plan.num_work = static_cast<uint32_t>(parts);
+    m->plan.num_reduce_rows = static_cast<uint32_t>(nred);
     m->plan.split_keys = static_cast<uint32_t>(L);
     m->plan.streaming = decode_streaming(m);
     m->plan.part_acc = m->d_part_acc;
     m->plan.part_ml = m->d_part_ml;
-    m->plan.needs_reduce = needs_reduce;
     m->decode_planned = true;
     return VO_OK;
 }
 
-// Prefill plan for the MFMA kernel: one item per 32-row query tile.  It needs
-// the layout PrefillMeta::new produces (paged.rs:128-141): the rows of
-// sequence s are seq_row_starts[s] .. seq_row_starts[s+1], row i of them at
-// position context_lens[s] + i with i + 1 + context_lens[s] keys.  Other
-// layouts run on the generic kernel.  Items are sorted by KV tiles, longest
-// first, so that the long ones are scheduled early.
-void plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens,
-                  const uint64_t *seq_row_starts) {
+vo_status plan_decode(vo_step_meta *m, Packer &pk) { return plan_decode_rows(m, pk, nullptr); }
+
+// Prefill plan.  It needs the layout PrefillMeta::new produces
+// (paged.rs:128-141): the rows of sequence s are seq_row_starts[s] ..
+// seq_row_starts[s+1], row i of them at position context_lens[s] + i with
+// i + 1 + context_lens[s] keys; other layouts run on the generic kernel.
+// A mixed continuous-batching step carries decode sequences (one new row) and
+// chunks in one call: a sequence with one row goes to the split-K decode
+// kernel, with the same split plan a decode call gives it, so its result is
+// bitwise the one decode_attention returns; sequences with more rows become
+// 64-row items of the MFMA prefill kernel, sorted by KV tiles, longest first,
+// so that the long ones are scheduled early.  Both kernels cover the same
+// shapes, and each row is written by exactly one of them.
+vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens,
+                       const uint64_t *seq_row_starts) {
     m->prefill_planned = false;
+    m->decode_planned = false;
     const uint64_t S = m->num_seqs;
     for (uint64_t s = 0; s < S; ++s) {
         for (uint64_t r = seq_row_starts[s]; r < seq_row_starts[s + 1]; ++r) {
             const uint64_t i = r - seq_row_starts[s];
-            if (m->row_seq[r] != s || m->row_num_keys[r] != context_lens[s] + i + 1) return;
+            if (m->row_seq[r] != s || m->row_num_keys[r] != context_lens[s] + i + 1) return VO_OK;
         }
     }
     const uint32_t QT = kernels::prefill_rows_per_tile();
     struct Item { uint32_t row, rows, pos, seq, tiles; };
     std::vector<Item> items;
+    m->decode_rows.clear();
+    // VO_PREFILL_DECODE_ROWS=0 keeps one-row sequences on the prefill kernel
+    // (a measurement switch).
+    const bool route_decode_rows = env_int("VO_PREFILL_DECODE_ROWS", 1) != 0;
     for (uint64_t s = 0; s < S; ++s) {
         const uint64_t n = seq_row_starts[s + 1] - seq_row_starts[s];
+        if (n == 1 && route_decode_rows) {
+            m->decode_rows.push_back(static_cast<uint32_t>(seq_row_starts[s]));
+            continue;
+        }
         for (uint64_t q0 = 0; q0 < n; q0 += QT) {
             Item it;
             it.row = static_cast<uint32_t>(seq_row_starts[s] + q0);
@@ -492,7 +520,10 @@ void plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens,
     }
     m->prefill_plan.work = dp;
     m->prefill_plan.num_items = static_cast<uint32_t>(items.size());
+    if (!m->decode_rows.empty())
+        if (vo_status rc = plan_decode_rows(m, pk, &m->decode_rows)) return rc;
     m->prefill_planned = true;
+    return VO_OK;
 }
 
 int decode_waves() {
@@ -534,7 +565,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
 
     const uint64_t u32s = (max_seqs + 1) + max_table_entries + 3 * max_rows  // offsets, tables, row arrays
                           + max_rows                                         // write slots
-                          + 2 * m->max_parts + 2 * max_rows                  // decode plan
+                          + 2 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
                           + 8 * 64;                                          // alignment slack
     m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
@@ -554,6 +585,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
         if (m->h_stage) (void)hipHostFree(m->h_stage);
         if (m->d_part_acc) (void)hipFree(m->d_part_acc);
         if (m->d_part_ml) (void)hipFree(m->d_part_ml);
+        if (m->copy_done) (void)hipEventDestroy(m->copy_done);
         delete m;
         return rc;
     }
@@ -594,7 +626,10 @@ extern "C" int32_t vo_step_meta_upload_prefill(
     if (vo_status rc = upload_common(m, kPrefill, op, block_size, num_seqs, table_off, tables,
                                      num_rows, slot_mapping, row_seq, row_num_keys, pk))
         return rc;
-    plan_prefill(m, pk, context_lens, seq_row_starts);
+    if (vo_status rc = plan_prefill(m, pk, context_lens, seq_row_starts)) {
+        m->kind = kNone;
+        return rc;
+    }
     if (!pk.fits()) {
         m->kind = kNone;
         return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
@@ -618,7 +653,7 @@ extern "C" int32_t vo_step_meta_upload_decode(vo_step_meta *m, uint64_t block_si
     if (vo_status rc = upload_common(m, kDecode, op, block_size, num_seqs, table_off, tables,
                                      num_seqs, slot_mapping, row_seq, row_num_keys, pk))
         return rc;
-    if (vo_status rc = plan_decode(m, pk, op)) {
+    if (vo_status rc = plan_decode(m, pk)) {
         m->kind = kNone;
         return rc;
     }
@@ -778,10 +813,20 @@ extern "C" int32_t vo_prefill_attention(const void *queries, uint64_t rows, uint
     if (m->prefill_planned &&
         kernels::prefill_mfma_supported(static_cast<uint32_t>(L.head_dim),
                                         static_cast<uint32_t>(L.block_size), group)) {
+        // A mixed step's chunks and decode rows write disjoint rows of `out`.
+        // (Running the two launches concurrently on two streams measured no
+        // faster: the decode workgroups take the CUs the long prefill
+        // workgroups need, and the chunks then finish last.)
+        const hipStream_t st = static_cast<hipStream_t>(stream);
         err = kernels::launch_prefill_mfma(pool->layer(layer), m->view, m->prefill_plan,
                                            static_cast<const uint16_t *>(queries),
-                                           static_cast<uint16_t *>(out), heads, scale,
-                                           static_cast<hipStream_t>(stream));
+                                           static_cast<uint16_t *>(out), heads, scale, st);
+        // Sequences with one new row (the decode rows of a mixed step).
+        if (err == hipSuccess && m->decode_planned)
+            err = kernels::launch_decode_mfma(pool->layer(layer), m->view, m->plan,
+                                              static_cast<const uint16_t *>(queries),
+                                              static_cast<uint16_t *>(out), heads, scale,
+                                              decode_waves(), st);
     } else {
         err = kernels::launch_attention_generic(
             pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),
@@ -818,6 +863,30 @@ extern "C" int32_t vo_decode_attention(const void *queries, uint64_t rows, uint6
             pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),
             static_cast<uint16_t *>(out), heads, scale, static_cast<hipStream_t>(stream));
     }
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_prefill_meta_build_device(
+    const uint32_t *seq_row_starts, const uint32_t *context_lens, const uint32_t *table_off,
+    const uint32_t *tables, uint64_t num_seqs, uint64_t num_rows, uint64_t block_size,
+    uint32_t *positions, uint32_t *slot_mapping, uint32_t *row_seq, uint32_t *row_num_keys,
+    uint32_t *errors, void *stream) {
+    const char *op = "prefill_meta_build_device";
+    if (num_rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!seq_row_starts || !context_lens || !table_off || !tables || !positions ||
+        !slot_mapping || !row_seq || !row_num_keys || !errors)
+        return fail_argument(op, "null device array");
+    if (num_seqs == 0 || block_size == 0) return fail_shape(op, "rows need a sequence and a block size");
+    if (num_seqs > kU32Limit || num_rows > kU32Limit || block_size > kU32Limit)
+        return fail_capacity("step metadata entries (u32)", std::max({num_seqs, num_rows, block_size}),
+                             kU32Limit);
+    const hipError_t err = kernels::launch_build_rows(
+        seq_row_starts, context_lens, table_off, tables, static_cast<uint32_t>(num_seqs),
+        static_cast<uint32_t>(num_rows), static_cast<uint32_t>(block_size), positions,
+        slot_mapping, row_seq, row_num_keys, errors, static_cast<hipStream_t>(stream));
     return device_status(op, err);
 }
 
