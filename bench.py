@@ -293,13 +293,52 @@ def bench_mixed(vo, W, orc, args):
     }
 
 
+def bench_rope_write(vo, W, orc, args):
+    """The layer step before attention (model.rs:307-311): rope(q); rope(k);
+    write_kv(k, v) as three launches, against the fused rope_write_kv, at the
+    decode (cfg2, 64 rows) and prefill (cfg3, 4096 rows) shapes."""
+    import torch
+    heads, kvh, hd, bs = 32, 8, 128, 16
+    table = vo.RopeTable(hd, 500000.0, 16384)
+    res = {}
+    for name, ctx, new in (("decode_64_rows", W.cfg2_context_lens(), None),
+                           ("prefill_4096_rows", W.cfg3_context_lens(), [512] * 8)):
+        kind = "decode" if new is None else "prefill"
+        backend = vo.HipBackend(device=0, max_seqs=len(ctx), max_rows=W.FILL_ROWS,
+                                max_table_entries=20000, max_query_heads=heads)
+        wl = W.build(vo, backend, kind=kind, heads=heads, kv_heads=kvh, head_dim=hd,
+                     block_size=bs, num_blocks=20000, context_lens=ctx, num_new=new, seed=7,
+                     keep_host=False)
+        q, k, v = wl.q.clone(), wl.k_new.clone(), wl.v_new.clone()
+
+        def unfused(i):
+            backend.rope(table, q, wl.pool, wl.meta, hd)
+            backend.rope(table, k, wl.pool, wl.meta, hd)
+            backend.write_kv(wl.pool, 0, k, v, wl.meta)
+
+        def fused(i):
+            backend.rope_write_kv(wl.pool, 0, table, q, k, v, wl.meta)
+
+        t_u = time_steps(torch, unfused, args.steps, args.warmup)
+        t_f = time_steps(torch, fused, args.steps, args.warmup)
+        rows = wl.rows
+        nbytes = rows * (heads * hd * 2 * 2 + kvh * hd * 2 * 2 * 2)
+        res[name] = {"rows": rows, "unfused_us": round(t_u * 1e6, 2), "fused_us": round(t_f * 1e6, 2),
+                     "fused_gbs": round(nbytes / t_f / 1e9, 1)}
+    return {"metric": "rope(q) + rope(k) + write_kv, fused vs three launches, 1 GPU",
+            "value": res["prefill_4096_rows"]["fused_us"], "unit": "us", "n_gpus": 1,
+            "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "Llama-3-8B shape: 32 q heads, 8 KV heads, head_dim 128, "
+                                   "theta 500000 llama3 scaling", "shapes": res}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=2, help="pool layers to rotate over")
-    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg5", "all"])
+    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg5", "rope", "all"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
@@ -349,6 +388,8 @@ def main():
         lines.append(bench_prefill(vo, W, orc, args))
     if args.config in ("cfg4a", "all"):
         lines.append(bench_mixed(vo, W, orc, args))
+    if args.config in ("rope", "all"):
+        lines.append(bench_rope_write(vo, W, orc, args))
     for line in lines:
         print(json.dumps(line), flush=True)
 

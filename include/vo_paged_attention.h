@@ -65,7 +65,8 @@ typedef enum vo_status {
     VO_ERR_BLOCK_OUT_OF_RANGE = 5,     /* EngineError::BlockOutOfRange  error.rs:29-34 */
     VO_ERR_DEVICE = 6,                 /* HIP runtime failure (no reference counterpart) */
     VO_ERR_INVALID_ARGUMENT = 7,       /* NULL pointer or zero size where one is required */
-    VO_ERR_UNSUPPORTED = 8             /* shape outside what the kernels are built for */
+    VO_ERR_UNSUPPORTED = 8,            /* shape outside what the kernels are built for */
+    VO_ERR_POSITION_OUT_OF_RANGE = 9   /* EngineError::PositionOutOfRange error.rs:52-53 */
 } vo_status;
 
 /* Detail of the last failed call on the calling thread.  The numeric fields
@@ -283,6 +284,55 @@ int32_t vo_decode_attention(const void *queries, uint64_t rows, uint64_t cols,
 int32_t vo_gather_kv(const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *meta,
                      uint64_t seq, uint64_t num_keys, void *out_keys, void *out_values,
                      void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Rotary position embedding (Backend::rope, mod.rs:105; rope.rs)      */
+/* ------------------------------------------------------------------ */
+
+/* The RoPE fields of ModelConfig (config.rs:9-34): head_dim, rope_theta and
+ * the llama3 rope_scaling block. */
+typedef struct vo_rope_config {
+    uint64_t head_dim;
+    double rope_theta;
+    double factor;
+    double low_freq_factor;
+    double high_freq_factor;
+    uint64_t original_max_position_embeddings;
+} vo_rope_config;
+
+/* Opaque: RopeTable (rope.rs:24-31) on one device, cos and sin
+ * [max_len][head_dim/2] f32, computed on the host in the reference's f32
+ * order (llama3_inv_freq rope.rs:36-60, RopeTable::new rope.rs:62-84) and
+ * copied to the device once (CpuBackend::new builds it once, cpu/mod.rs:53). */
+typedef struct vo_rope_table vo_rope_table;
+
+int32_t vo_rope_table_create(const vo_rope_config *config, uint64_t max_len, int32_t device,
+                             vo_rope_table **out);
+void vo_rope_table_destroy(vo_rope_table *table);
+
+/* Backend::rope (mod.rs:105; cpu/mod.rs:231-255; shape checks
+ * arena/ops.rs:83-99): rotates x [rows, cols] bf16 in place, every head of
+ * width head_dim, row r at the position the step metadata gives it
+ * (vo_step_meta_upload_prefill / _decode positions; rows == the meta's rows).
+ * f32 arithmetic in the reference's order, result rounded to bf16.
+ * Errors: VO_ERR_SHAPE (positions != rows, head_dim odd or zero or not
+ * dividing cols, or head_dim != the table's), VO_ERR_POSITION_OUT_OF_RANGE
+ * {value = pos, limit = max_len} for the first position past the table. */
+int32_t vo_rope(const vo_rope_table *table, void *x, uint64_t rows, uint64_t cols,
+                uint64_t head_dim, const vo_step_meta *meta, void *stream);
+
+/* The layer's "rope(q); rope(k); write_kv(k, v)" (model.rs:307-311) as one
+ * launch.  No counterpart in the reference's op list: it fuses three of its
+ * ops.  queries [rows, q_cols] are rotated in place (as Backend::rope leaves
+ * them); keys [rows, kv_cols] are read, rotated and written to the pool with
+ * values; the caller's keys buffer itself is left unrotated (the reference
+ * never reads k after write_kv).  Checks are those of vo_rope on both
+ * operands and of vo_write_kv, in that order, all before the launch.
+ * Needs block size 16 and head_dim 64 or 128 (else VO_ERR_UNSUPPORTED; use
+ * vo_rope twice and vo_write_kv). */
+int32_t vo_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_rope_table *table,
+                         void *queries, uint64_t q_cols, const void *keys, const void *values,
+                         uint64_t rows, uint64_t kv_cols, const vo_step_meta *meta, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Opt-in kernel timing (the reference's opt-in per-op timing,         */

@@ -82,6 +82,10 @@ def _load():
         "vo_oracle_naive_attend_f64": (None, [_f32p, _f32p, _f32p, _u64, _u64, _u64, _u64,
                                               _f32p]),
         "vo_oracle_splitk_combine": (None, [_u64, _u64, _f32p, _f32p, _f32p, _f32p]),
+        "vo_oracle_rope_inv_freq": (None, [_u64, ctypes.c_double, ctypes.c_double,
+                                           ctypes.c_double, ctypes.c_double, _u64, _f32p]),
+        "vo_oracle_rope_table": (None, [_f32p, _u64, _u64, _f32p, _f32p]),
+        "vo_oracle_rope_apply": (None, [_f32p, _u64, _u64, _u32p, _f32p, _f32p, _u64]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(h, name)
@@ -275,3 +279,40 @@ def splitk_combine(m, l, acc) -> np.ndarray:
     out = np.zeros(hd, np.float32)
     lib.vo_oracle_splitk_combine(len(m), hd, _pf(m), _pf(l), _pf(acc), _pf(out))
     return out
+
+
+# ---- cpu/rope.rs ------------------------------------------------------------
+
+# config.rs:41-56 (LLAMA_3_2_1B) rope_scaling; BASELINE's models use theta
+# 10000 (config 1) and 500000 (config 4) with the same scaling block.
+LLAMA3_SCALING = dict(factor=32.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                      original_max_position_embeddings=8192)
+
+
+def rope_inv_freq(head_dim: int, theta: float, factor=32.0, low_freq_factor=1.0,
+                  high_freq_factor=4.0, original_max_position_embeddings=8192) -> np.ndarray:
+    """rope.rs:36-60 (llama3_inv_freq)."""
+    out = np.zeros(head_dim // 2, np.float32)
+    lib.vo_oracle_rope_inv_freq(head_dim, theta, factor, low_freq_factor, high_freq_factor,
+                                original_max_position_embeddings, _pf(out))
+    return out
+
+
+def rope_table(inv_freq, max_len: int):
+    """rope.rs:62-84 (RopeTable::new): (cos, sin), each [max_len, half] f32."""
+    inv = _f32(inv_freq)
+    half = inv.size
+    c = np.zeros((max_len, half), np.float32)
+    sn = np.zeros((max_len, half), np.float32)
+    lib.vo_oracle_rope_table(_pf(inv), half, max_len, _pf(c), _pf(sn))
+    return c, sn
+
+
+def rope_apply(x, positions, cos_tab, sin_tab) -> np.ndarray:
+    """rope.rs:86-100 (RopeTable::apply) on every row of x [rows, cols]; a copy."""
+    x = _f32(x).copy()
+    pos = _u32(positions)
+    c, sn = _f32(cos_tab), _f32(sin_tab)
+    lib.vo_oracle_rope_apply(_pf(x), x.shape[0], x.shape[1], _p32(pos), _pf(c), _pf(sn),
+                             c.shape[1])
+    return x

@@ -12,6 +12,7 @@
  *   backend/cpu/attention.rs  paged_attention, attend_one_row,
  *                             check_block_tables
  *   backend/cpu/tests.rs  naive_attend (the reference's f64 test oracle)
+ *   backend/cpu/rope.rs   llama3_inv_freq, RopeTable::new / apply
  */
 #include "vo_oracle.h"
 
@@ -360,5 +361,69 @@ void vo_oracle_splitk_combine(uint64_t splits, uint64_t head_dim, const float *m
         for (uint64_t i = 0; i < splits; ++i)
             if (m[i] != -INFINITY) num += exp((double)m[i] - big) * (double)acc[i * head_dim + d];
         out[d] = (float)(num / denom);
+    }
+}
+
+
+/* ---- backend/cpu/rope.rs --------------------------------------------- */
+
+/* rope.rs:36-60.  Every operation is the reference's f32 operation in the
+ * reference's order: `1.0 / base.powf((2 * i) as f32 / d as f32)`,
+ * `2.0 * PI / inv`, and `(1.0 - smooth) * inv / factor + smooth * inv`
+ * evaluated left to right (no contraction: -ffp-contract=off). */
+void vo_oracle_rope_inv_freq(uint64_t head_dim, double theta, double factor, double low,
+                             double high, uint64_t old_ctx, float *out) {
+    const float d = (float)head_dim;
+    const float base = (float)theta;
+    const float f = (float)factor;
+    const float lo = (float)low;
+    const float hi = (float)high;
+    const float ctx = (float)old_ctx;
+    const float low_freq_wavelen = ctx / lo;
+    const float high_freq_wavelen = ctx / hi;
+    const float pi = 3.14159265358979323846f; /* std::f32::consts::PI */
+    for (uint64_t i = 0; i < head_dim / 2; ++i) {
+        const float inv = 1.0f / powf(base, (float)(2 * i) / d);
+        const float wavelen = 2.0f * pi / inv;
+        float r;
+        if (wavelen < high_freq_wavelen) {
+            r = inv;
+        } else if (wavelen > low_freq_wavelen) {
+            r = inv / f;
+        } else {
+            const float smooth = (ctx / wavelen - lo) / (hi - lo);
+            r = (1.0f - smooth) * inv / f + smooth * inv;
+        }
+        out[i] = r;
+    }
+}
+
+/* rope.rs:62-84: theta = p as f32 * inv_freq[i]; cos and sin from libm. */
+void vo_oracle_rope_table(const float *inv_freq, uint64_t half, uint64_t max_len, float *cos_out,
+                          float *sin_out) {
+    for (uint64_t p = 0; p < max_len; ++p) {
+        for (uint64_t i = 0; i < half; ++i) {
+            const float th = (float)p * inv_freq[i];
+            cos_out[p * half + i] = cosf(th);
+            sin_out[p * half + i] = sinf(th);
+        }
+    }
+}
+
+/* rope.rs:86-100: x1' = a*cos - b*sin, x2' = b*cos + a*sin per pair. */
+void vo_oracle_rope_apply(float *x, uint64_t rows, uint64_t cols, const uint32_t *positions,
+                          const float *cos_tab, const float *sin_tab, uint64_t half) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        const float *c = cos_tab + (uint64_t)positions[r] * half;
+        const float *sn = sin_tab + (uint64_t)positions[r] * half;
+        for (uint64_t h0 = 0; h0 + 2 * half <= cols; h0 += 2 * half) {
+            float *x1 = x + r * cols + h0;
+            float *x2 = x1 + half;
+            for (uint64_t i = 0; i < half; ++i) {
+                const float a = x1[i], b = x2[i];
+                x1[i] = a * c[i] - b * sn[i];
+                x2[i] = b * c[i] + a * sn[i];
+            }
+        }
     }
 }

@@ -131,6 +131,24 @@ void vo_oracle_naive_attend_f64(const float *q, const float *seq_k, const float 
 void vo_oracle_splitk_combine(uint64_t splits, uint64_t head_dim, const float *m,
                               const float *l, const float *acc, float *out);
 
+/* ---- backend/cpu/rope.rs --------------------------------------------- */
+
+/* rope.rs:36-60 (llama3_inv_freq): out[i], i < head_dim/2, the Llama 3 scaled
+ * inverse frequencies.  theta, factor, low, high are the config's f64
+ * values, narrowed to f32 as the reference does; old_ctx is
+ * original_max_position_embeddings. */
+void vo_oracle_rope_inv_freq(uint64_t head_dim, double theta, double factor, double low,
+                             double high, uint64_t old_ctx, float *out);
+
+/* rope.rs:62-84 (RopeTable::new): cos, sin [max_len][half], theta = p * f. */
+void vo_oracle_rope_table(const float *inv_freq, uint64_t half, uint64_t max_len, float *cos_out,
+                          float *sin_out);
+
+/* rope.rs:86-100 (RopeTable::apply) on rows [rows][cols]: each head of width
+ * 2*half rotated at positions[r]. */
+void vo_oracle_rope_apply(float *x, uint64_t rows, uint64_t cols, const uint32_t *positions,
+                          const float *cos_tab, const float *sin_tab, uint64_t half);
+
 #ifdef __cplusplus
 }
 #endif

@@ -509,3 +509,123 @@ def test_device_meta_flags_uncovered_rows(vo):
     assert err == 1
     assert list(slot[:4]) == [28, 29, 30, 31] and slot[4] == 0xffffffff
 
+
+
+# ---------------------------------------------------------------------------
+# RoPE (rope.rs) alone and fused with the cache write
+# ---------------------------------------------------------------------------
+def _bf16_bits_of(x):
+    """Round f32 -> bf16 (nearest even), as uint16 bit patterns."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def _as_f32(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("hd,theta,cols_heads", [(128, 500000.0, 32), (64, 10000.0, 4),
+                                                 (8, 10000.0, 6), (128, 10000.0, 8)])
+def test_rope_bit_exact_vs_oracle(vo, gpu_backend, hd, theta, cols_heads):
+    """Backend::rope on bf16 rows equals the oracle's f32 rotation of the same
+    values, rounded to bf16, bit for bit (cpu/mod.rs:231-255, rope.rs:86-100)."""
+    import torch
+    _say(f"rope hd={hd} theta={theta}")
+    max_len = 9000
+    table = vo.RopeTable(hd, theta, max_len)
+    rng = np.random.default_rng(hd)
+    ctx = [0, 5, 700, 4095, 8000]
+    new = [40, 1, 33, 1, 999]
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=cols_heads, kv_heads=2 if hd == 8 else 1,
+                 head_dim=hd, block_size=16, num_blocks=1000, context_lens=ctx, num_new=new,
+                 seed=hd + 1, keep_host=False)
+    x = torch.tensor(rng.standard_normal((wl.rows, cols_heads * hd)), dtype=torch.float32,
+                     device="cuda:0").to(torch.bfloat16)
+    x0 = _as_f32(x)
+    gpu_backend.rope(table, x, wl.pool, wl.meta, hd)
+    torch.cuda.synchronize()
+    c, s = orc.rope_table(orc.rope_inv_freq(hd, theta), max_len)
+    want = _bf16_bits_of(orc.rope_apply(x0, wl.meta.positions, c, s))
+    assert np.array_equal(_bits(x).view(np.uint16), want)
+
+
+def test_rope_errors_match_reference(vo, gpu_backend):
+    """PositionOutOfRange {pos, max} for the first position past the table
+    (cpu/mod.rs:241-246); Shape for a head_dim the table was not built for."""
+    import torch
+    _say("rope errors")
+    table = vo.RopeTable(64, 10000.0, 100)
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=2, kv_heads=1, head_dim=64,
+                 block_size=16, num_blocks=64, context_lens=[90], num_new=[20], seed=5,
+                 keep_host=False)
+    x = torch.zeros((20, 128), dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(vo.PositionOutOfRange) as e:
+        gpu_backend.rope(table, x, wl.pool, wl.meta, 64)
+    assert e.value.value == 100 and e.value.limit == 100
+    with pytest.raises(vo.ShapeError):
+        gpu_backend.rope(table, x, wl.pool, wl.meta, 32)
+
+
+@pytest.mark.parametrize("hd,heads,kvh", [(128, 32, 8), (64, 4, 2), (128, 64, 8)])
+def test_rope_write_kv_fused_matches_unfused(vo, gpu_backend, hd, heads, kvh):
+    """The fused launch leaves q and the pool bitwise as rope(q); rope(k);
+    write_kv(k, v) does (model.rs:307-311), on a mixed step (chunks that start
+    mid-block, whole blocks, decode rows)."""
+    import torch
+    _say(f"rope_write_kv hd={hd} heads={heads}")
+    table = vo.RopeTable(hd, 500000.0, 6000)
+    ctx = [0, 3, 16, 100, 2000, 777, 15]
+    new = [70, 1, 33, 1, 129, 1, 17]
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=16, num_blocks=900, context_lens=ctx, num_new=new, seed=hd + heads,
+                 num_layers=2, keep_host=False)
+    k = wl.k_new.clone()
+    v = wl.v_new.clone()
+    q_ref = wl.q.clone()
+    gpu_backend.rope(table, q_ref, wl.pool, wl.meta, hd)
+    k_rot = k.clone()
+    gpu_backend.rope(table, k_rot, wl.pool, wl.meta, hd)
+    gpu_backend.write_kv(wl.pool, 0, k_rot, v, wl.meta)
+    q_fused = wl.q.clone()
+    gpu_backend.rope_write_kv(wl.pool, 1, table, q_fused, k, v, wl.meta)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(q_fused), _bits(q_ref))
+    assert np.array_equal(_bits(k), _bits(wl.k_new))  # the caller's keys stay unrotated
+    for s in range(len(ctx)):
+        n = ctx[s] + new[s]
+        meta = wl.meta
+        k0, v0 = gpu_backend.read_kv(wl.pool, 0, meta, s, n)
+        k1, v1 = gpu_backend.read_kv(wl.pool, 1, meta, s, n)
+        lo = ctx[s]
+        assert np.array_equal(_bits(k1[lo:]), _bits(k0[lo:])), s
+        assert np.array_equal(_bits(v1[lo:]), _bits(v0[lo:])), s
+
+
+def test_rope_write_kv_repeated_slot_rotates_every_q_row(vo, gpu_backend):
+    """A slot given twice keeps the later row in the cache (cpu/mod.rs:277-283)
+    while both rows' q are rotated."""
+    import torch
+    _say("rope_write_kv repeated slot")
+    hd, heads, kvh = 128, 8, 2
+    table = vo.RopeTable(hd, 500000.0, 64)
+    layout = vo.KvLayout(1, 8, 16, kvh, hd)
+    pool = gpu_backend.alloc_kv_pool(layout)
+    meta = vo.PrefillMeta.new([vo.PrefillSeq(0, 3, [5])], 16)
+    meta.slot_mapping[:] = [80, 81, 80]
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(9)
+    q = torch.randn((3, heads * hd), generator=g, device="cuda:0").to(torch.bfloat16)
+    k = torch.randn((3, kvh * hd), generator=g, device="cuda:0").to(torch.bfloat16)
+    v = torch.randn((3, kvh * hd), generator=g, device="cuda:0").to(torch.bfloat16)
+    q_ref = q.clone()
+    gpu_backend.rope(table, q_ref, pool, meta, hd)
+    gpu_backend.rope_write_kv(pool, 0, table, q, k, v, meta)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(q), _bits(q_ref))
+    kc, vc = gpu_backend.read_kv(pool, 0, meta, 0, 2)
+    c, s = orc.rope_table(orc.rope_inv_freq(hd, 500000.0), 64)
+    k_rot = _bf16_bits_of(orc.rope_apply(_as_f32(k), [0, 1, 2], c, s))
+    assert np.array_equal(_bits(kc[0:1]).view(np.uint16), k_rot[2:3])
+    assert np.array_equal(_bits(kc[1:2]).view(np.uint16), k_rot[1:2])
+    assert np.array_equal(_bits(vc[0:1]), _bits(v[2:3]))

@@ -49,6 +49,7 @@ VO_ERR_BLOCK_OUT_OF_RANGE = 5
 VO_ERR_DEVICE = 6
 VO_ERR_INVALID_ARGUMENT = 7
 VO_ERR_UNSUPPORTED = 8
+VO_ERR_POSITION_OUT_OF_RANGE = 9
 
 _u64 = ctypes.c_uint64
 _u32p = ctypes.POINTER(ctypes.c_uint32)
@@ -72,6 +73,12 @@ class vo_kv_layout(ctypes.Structure):
 class vo_kernel_stat(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 48), ("calls", _u64), ("total_ms", ctypes.c_double),
                 ("min_ms", ctypes.c_double), ("max_ms", ctypes.c_double)]
+
+
+class vo_rope_config(ctypes.Structure):
+    _fields_ = [("head_dim", _u64), ("rope_theta", ctypes.c_double), ("factor", ctypes.c_double),
+                ("low_freq_factor", ctypes.c_double), ("high_freq_factor", ctypes.c_double),
+                ("original_max_position_embeddings", _u64)]
 
 
 class vo_prefill_seq(ctypes.Structure):
@@ -115,6 +122,12 @@ SIGNATURES = {
     "vo_gather_kv": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _vp, _vp, _vp]),
     "vo_prefill_meta_build_device": (ctypes.c_int32, [_vp, _vp, _vp, _vp, _u64, _u64, _u64,
                                                       _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vo_rope_table_create": (ctypes.c_int32, [ctypes.POINTER(vo_rope_config), _u64,
+                                              ctypes.c_int32, ctypes.POINTER(_vp)]),
+    "vo_rope_table_destroy": (None, [_vp]),
+    "vo_rope": (ctypes.c_int32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp]),
+    "vo_rope_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _vp, _vp, _u64, _u64, _vp,
+                                          _vp]),
     "vo_profiling_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "vo_profile_read": (ctypes.c_int32, [ctypes.POINTER(vo_kernel_stat), _u64, _u64p]),
     "vo_profile_reset": (None, []),
@@ -187,6 +200,7 @@ class BlockOutOfRange(EngineError): pass
 class DeviceError(EngineError): pass
 class InvalidArgument(EngineError): pass
 class Unsupported(EngineError): pass
+class PositionOutOfRange(EngineError): pass
 
 
 _ERROR_CLASSES = {
@@ -194,6 +208,7 @@ _ERROR_CLASSES = {
     VO_ERR_BLOCK_TABLE_TOO_SHORT: BlockTableTooShort, VO_ERR_SLOT_OUT_OF_RANGE: SlotOutOfRange,
     VO_ERR_BLOCK_OUT_OF_RANGE: BlockOutOfRange, VO_ERR_DEVICE: DeviceError,
     VO_ERR_INVALID_ARGUMENT: InvalidArgument, VO_ERR_UNSUPPORTED: Unsupported,
+    VO_ERR_POSITION_OUT_OF_RANGE: PositionOutOfRange,
 }
 
 
@@ -488,6 +503,36 @@ def _dev_ptr(t) -> _vp:
     return _vp(t.data_ptr())
 
 
+class RopeTable:
+    """RopeTable (rope.rs:24-100) on one device: Llama 3 scaled frequencies,
+    cos/sin for positions 0 .. max_len-1.  Defaults are LLAMA_3_2_1B's
+    rope_scaling block (config.rs:41-56)."""
+
+    def __init__(self, head_dim: int, rope_theta: float, max_len: int, device: int = 0,
+                 factor: float = 32.0, low_freq_factor: float = 1.0,
+                 high_freq_factor: float = 4.0, original_max_position_embeddings: int = 8192):
+        cfg = vo_rope_config(head_dim, rope_theta, factor, low_freq_factor, high_freq_factor,
+                             original_max_position_embeddings)
+        self._h = _vp()
+        _check(lib.vo_rope_table_create(ctypes.byref(cfg), max_len, device, ctypes.byref(self._h)))
+        self.head_dim, self.max_len = head_dim, max_len
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_rope_table_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class HipBackend:
     """The attention-path ops of ``trait Backend`` (mod.rs:61-182) on one GPU.
 
@@ -554,6 +599,23 @@ class HipBackend:
         _check(fn(_dev_ptr(queries), queries.shape[0], queries.shape[1], pool.handle, layer,
                   m.handle, _dev_ptr(out), _stream_ptr(stream)))
         return out
+
+    # mod.rs:105
+    def rope(self, table: RopeTable, x, pool: KvPool, meta, head_dim: int, stream=None) -> None:
+        """Backend::rope: rotates x [rows, cols] in place at the meta's positions."""
+        m = self._meta_for(pool, meta, stream)
+        _check(lib.vo_rope(table.handle, _dev_ptr(x), x.shape[0], x.shape[1], head_dim, m.handle,
+                           _stream_ptr(stream)))
+
+    def rope_write_kv(self, pool: KvPool, layer: int, table: RopeTable, queries, keys, values,
+                      meta, stream=None) -> None:
+        """rope(q); rope(k); write_kv(k, v) in one launch (q rotated in place)."""
+        m = self._meta_for(pool, meta, stream)
+        if tuple(values.shape) != tuple(keys.shape):
+            raise ValueError("keys and values must have the same shape")
+        _check(lib.vo_rope_write_kv(pool.handle, layer, table.handle, _dev_ptr(queries),
+                                    queries.shape[1], _dev_ptr(keys), _dev_ptr(values),
+                                    keys.shape[0], keys.shape[1], m.handle, _stream_ptr(stream)))
 
     # mod.rs:121-135
     def prefill_attention(self, queries, pool: KvPool, layer: int, meta: PrefillMeta, out=None,

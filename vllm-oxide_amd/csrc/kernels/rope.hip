@@ -1,0 +1,263 @@
+// rope.hip -- rotary position embedding on bf16 rows, alone (Backend::rope)
+// and fused with the paged KV-cache write.
+//
+// Math (crates/engine/src/backend/cpu/rope.rs:86-100): each head vector of
+// width d = 2*half splits into x1 = x[..half], x2 = x[half..]; pair i at
+// position p uses the precomputed cos/sin of table row p:
+//   x1'[i] = x1[i]*cos - x2[i]*sin,   x2'[i] = x2[i]*cos + x1[i]*sin.
+// Every product and sum is a separately rounded f32 operation in that order
+// (no contraction into FMA), as the reference
+// computes, so the f32 result equals the reference's on the same inputs; it
+// is then rounded to bf16 (round to nearest even).
+//
+// rope_rows_kernel: one thread per (row, head, 8 pairs), or per pair when
+// half is not a multiple of 8; 16-byte loads and stores in the first case.
+// rope_cache_kernel: the layer's "rope(q); rope(k); write_kv(k, v)"
+// (model.rs:307-311) as one launch over the step's write plan: one wavefront
+// per (run of rows with consecutive slots in one block, KV head).  A lane
+// owns 8 dims of a row; its rotation partner (the other half of the head) is
+// the lane UPR/2 away in the same row, reached with a lane shuffle.  The
+// wavefront rotates the run's q rows for the G query heads of its KV head in
+// place, writes the rotated K into the key-major tile and V into the
+// dim-major tile (transposed in registers, 32-byte runs per dim for a whole
+// block), reading each row's cos/sin once.
+//
+// Roofline: HBM.  Bytes per row = q read + written, k and v read and written
+// to the pool, cos/sin 2*half*4*2 (mostly cache hits).
+#include "vo_device.hpp"
+#include "vo_kernels.hpp"
+
+namespace vo {
+namespace kernels {
+
+namespace {
+
+__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(a)) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
+}
+
+// x1' (first half) and x2' (second half) of rope.rs:95-96.  HIP compiles
+// with contraction on, which would fuse a product into the following add
+// (an FMA rounds once where the reference rounds twice); the pragma keeps
+// each product and sum rounded on its own.
+__device__ __forceinline__ float rot_first(float a, float b, float c, float s) {
+#pragma clang fp contract(off)
+    const float ac = a * c;
+    const float bs = b * s;
+    return ac - bs;
+}
+__device__ __forceinline__ float rot_second(float a, float b, float c, float s) {
+#pragma clang fp contract(off)
+    const float bc = b * c;
+    const float as = a * s;
+    return bc + as;
+}
+
+// 8 pairs: x1 = a (8 bf16), x2 = b (8 bf16) -> rotated in place.
+__device__ __forceinline__ void rotate8(u32x4 &a, u32x4 &b, const float *c, const float *s) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float a0 = lo_f(a[k]), a1 = hi_f(a[k]);
+        const float b0 = lo_f(b[k]), b1 = hi_f(b[k]);
+        const float c0 = c[2 * k], c1 = c[2 * k + 1], s0 = s[2 * k], s1 = s[2 * k + 1];
+        a[k] = pack2(rot_first(a0, b0, c0, s0), rot_first(a1, b1, c1, s1));
+        b[k] = pack2(rot_second(a0, b0, c0, s0), rot_second(a1, b1, c1, s1));
+    }
+}
+
+template <bool WIDE>
+__global__ __launch_bounds__(256) void rope_rows_kernel(uint16_t *__restrict__ x, uint32_t rows,
+                                                        uint32_t cols, uint32_t half,
+                                                        const uint32_t *__restrict__ positions,
+                                                        const float *__restrict__ cos_tab,
+                                                        const float *__restrict__ sin_tab) {
+    constexpr uint32_t PW = WIDE ? 8 : 1;  // pairs per thread
+    const uint32_t chunks = half / PW;
+    const uint32_t heads = cols / (2 * half);
+    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<uint64_t>(rows) * heads * chunks) return;
+    const uint32_t row = static_cast<uint32_t>(idx / (static_cast<uint64_t>(heads) * chunks));
+    const uint32_t rem = static_cast<uint32_t>(idx % (static_cast<uint64_t>(heads) * chunks));
+    const uint32_t head = rem / chunks;
+    const uint32_t p0 = (rem % chunks) * PW;
+    uint16_t *h = x + static_cast<uint64_t>(row) * cols + static_cast<uint64_t>(head) * 2 * half;
+    const uint64_t t = static_cast<uint64_t>(positions[row]) * half + p0;
+    if constexpr (WIDE) {
+        float c[8], s[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            c[k] = cos_tab[t + k];
+            s[k] = sin_tab[t + k];
+        }
+        u32x4 a = *reinterpret_cast<const u32x4 *>(h + p0);
+        u32x4 b = *reinterpret_cast<const u32x4 *>(h + half + p0);
+        rotate8(a, b, c, s);
+        *reinterpret_cast<u32x4 *>(h + p0) = a;
+        *reinterpret_cast<u32x4 *>(h + half + p0) = b;
+    } else {
+        const float c = cos_tab[t], s = sin_tab[t];
+        const float a = bf16_bits_to_f32(h[p0]), b = bf16_bits_to_f32(h[half + p0]);
+        h[p0] = f32_to_bf16_bits(rot_first(a, b, c, s));
+        h[half + p0] = f32_to_bf16_bits(rot_second(a, b, c, s));
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void rope_cache_kernel(
+    uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool, uint32_t kv_heads,
+    uint16_t *__restrict__ q, uint32_t q_cols, uint32_t group, const uint16_t *__restrict__ keys,
+    const uint16_t *__restrict__ values, const uint32_t *__restrict__ segments,
+    const uint32_t *__restrict__ positions, const float *__restrict__ cos_tab,
+    const float *__restrict__ sin_tab, uint32_t num_items) {
+    constexpr uint32_t BS = 16;
+    constexpr uint32_t HALF = HD / 2;
+    constexpr int DPL = HD / 64;        // V dims per lane
+    constexpr uint32_t UPR = HD / 8;    // 16-byte units per row of one head
+    constexpr uint32_t RPI = 64 / UPR;  // rows per instruction
+    constexpr uint32_t KI = BS / RPI;
+    const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= num_items) return;  // whole wavefront
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t seg = item / kv_heads;
+    const uint32_t kvh = item % kv_heads;
+    const uint32_t row0 = segments[3 * seg];
+    const uint32_t n = segments[3 * seg + 1];  // 1 .. BS
+    const uint32_t slot0 = segments[3 * seg + 2];
+    // A superseded row (slot kSkipSlot) only has its q rotated.
+    const bool cache = slot0 != kSkipSlot;
+    const uint32_t off0 = cache ? slot0 % BS : 0;
+    const uint64_t width = static_cast<uint64_t>(kv_heads) * HD;
+    const uint64_t tile = cache ? (static_cast<uint64_t>(slot0 / BS) * kv_heads + kvh) * (BS * HD) : 0;
+
+    const uint32_t u = lane % UPR;
+    const bool first_half = u < UPR / 2;
+    const uint32_t d = 8 * u;
+    const uint32_t p0 = 8 * (u % (UPR / 2));  // first pair of the lane's 8 dims
+    const uint32_t i0 = lane / UPR;
+
+    // Rotates a lane's 8 dims with its partner lane's (the other half).
+    auto rot = [&](u32x4 own, const float *c, const float *s) -> u32x4 {
+        u32x4 other;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) other[k] = __shfl_xor(own[k], UPR / 2, 64);
+        u32x4 a = first_half ? own : other;
+        u32x4 b = first_half ? other : own;
+        rotate8(a, b, c, s);
+        return first_half ? a : b;
+    };
+
+#pragma unroll
+    for (uint32_t j = 0; j < KI; ++j) {
+        const uint32_t i = i0 + RPI * j;
+        // Every lane of a row takes part in the shuffles, so rows past the
+        // run clamp to its last row and skip only the stores.
+        const bool live = i < n;
+        const uint32_t row = row0 + min(i, n - 1);
+        const uint64_t t = static_cast<uint64_t>(positions[row]) * HALF + p0;
+        float c[8], s[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            c[k] = cos_tab[t + k];
+            s[k] = sin_tab[t + k];
+        }
+        const u32x4 kin = *reinterpret_cast<const u32x4 *>(keys + row * width + kvh * HD + d);
+        const u32x4 kout = rot(kin, c, s);
+        if (live && cache)
+            *reinterpret_cast<u32x4 *>(k_pool + tile + (d / 32) * (BS * 32) + (off0 + i) * 32 + d % 32) = kout;
+        for (uint32_t h = 0; h < group; ++h) {
+            uint16_t *qp = q + static_cast<uint64_t>(row) * q_cols + (kvh * group + h) * HD + d;
+            const u32x4 qin = *reinterpret_cast<const u32x4 *>(qp);
+            const u32x4 qout = rot(qin, c, s);
+            if (live) *reinterpret_cast<u32x4 *>(qp) = qout;
+        }
+    }
+
+    if (!cache) return;
+    uint16_t vv[DPL][BS];
+    const uint16_t *vsrc = values + static_cast<uint64_t>(row0) * width + kvh * HD + DPL * lane;
+#pragma unroll
+    for (uint32_t i = 0; i < BS; ++i) {
+        if (i < n) {
+            if constexpr (DPL == 2) {
+                const uint32_t w = *reinterpret_cast<const uint32_t *>(vsrc + i * width);
+                vv[0][i] = static_cast<uint16_t>(w & 0xffffu);
+                vv[1][i] = static_cast<uint16_t>(w >> 16);
+            } else {
+                vv[0][i] = vsrc[i * width];
+            }
+        }
+    }
+    uint16_t *vdst = v_pool + tile + static_cast<uint64_t>(DPL * lane) * BS;
+    if (n == BS) {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+            u32x4 lo, hi;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                lo[p] = static_cast<uint32_t>(vv[e][2 * p]) | (static_cast<uint32_t>(vv[e][2 * p + 1]) << 16);
+                hi[p] = static_cast<uint32_t>(vv[e][8 + 2 * p]) |
+                        (static_cast<uint32_t>(vv[e][8 + 2 * p + 1]) << 16);
+            }
+            *reinterpret_cast<u32x4 *>(vdst + e * BS) = lo;
+            *reinterpret_cast<u32x4 *>(vdst + e * BS + 8) = hi;
+        }
+    } else {
+#pragma unroll
+        for (uint32_t i = 0; i < BS; ++i) {
+            if (i < n) {
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) vdst[e * BS + off0 + i] = vv[e][i];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_rope_rows(uint16_t *x, uint32_t rows, uint32_t cols, uint32_t half,
+                            const uint32_t *positions, const float *cos_tab, const float *sin_tab,
+                            hipStream_t stream) {
+    if (rows == 0 || cols == 0) return hipSuccess;
+    if (half == 0 || cols % (2 * half) != 0) return hipErrorInvalidValue;
+    const bool wide = half % 8 == 0;
+    const uint64_t per_row = static_cast<uint64_t>(cols / (2 * half)) * (wide ? half / 8 : half);
+    const uint64_t grid = (static_cast<uint64_t>(rows) * per_row + 255) / 256;
+    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
+    KernelTimer timer("rope", stream);
+    if (wide)
+        hipLaunchKernelGGL((rope_rows_kernel<true>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                           stream, x, rows, cols, half, positions, cos_tab, sin_tab);
+    else
+        hipLaunchKernelGGL((rope_rows_kernel<false>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                           stream, x, rows, cols, half, positions, cos_tab, sin_tab);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_cache(const PoolLayer &pool, uint16_t *q, uint32_t q_cols, uint32_t group,
+                             const uint16_t *keys, const uint16_t *values, const WritePlan &plan,
+                             const uint32_t *positions, const float *cos_tab, const float *sin_tab,
+                             hipStream_t stream) {
+    if (plan.num_segments == 0) return hipSuccess;
+    if (!cache_write_supported(pool.head_dim, pool.block_size)) return hipErrorInvalidValue;
+    const uint64_t items = static_cast<uint64_t>(plan.num_segments) * pool.kv_heads;
+    const uint64_t grid = (items + 3) / 4;
+    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
+    KernelTimer timer("rope_cache", stream);
+    if (pool.head_dim == 128)
+        hipLaunchKernelGGL((rope_cache_kernel<128>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                           stream, pool.k, pool.v, pool.kv_heads, q, q_cols, group, keys, values,
+                           plan.segments, positions, cos_tab, sin_tab,
+                           static_cast<uint32_t>(items));
+    else
+        hipLaunchKernelGGL((rope_cache_kernel<64>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+                           stream, pool.k, pool.v, pool.kv_heads, q, q_cols, group, keys, values,
+                           plan.segments, positions, cos_tab, sin_tab,
+                           static_cast<uint32_t>(items));
+    return hipGetLastError();
+}
+
+}  // namespace kernels
+}  // namespace vo

@@ -43,9 +43,38 @@ struct MetaView {
     const uint32_t *row_seq;       // [T]
     const uint32_t *row_num_keys;  // [T]
     const uint32_t *slot_mapping;  // [T]
+    const uint32_t *positions;     // [T] (RoPE); null for a slots-only upload
     uint32_t num_rows;
     uint32_t num_seqs;
 };
+
+// Write plan of one step's write_kv: runs of rows whose slots are
+// consecutive inside one block (rows never cross a block boundary).
+struct WritePlan {
+    const uint32_t *segments;  // [num_segments][3]: (first row, rows, first slot)
+    uint32_t num_segments;
+};
+
+// True when the block-run cache writer covers this shape.
+bool cache_write_supported(uint32_t head_dim, uint32_t block_size);
+
+// reshape_and_cache over a write plan: one wavefront per (run, KV head); K
+// goes out in 16-byte stores, V is transposed in registers so that a whole
+// block writes each dim's keys as one 32-byte run.
+hipError_t launch_cache_write(const PoolLayer &pool, const uint16_t *keys, const uint16_t *values,
+                              const WritePlan &plan, hipStream_t stream);
+
+// RoPE (rope.rs:86-100) in place on x [rows, cols] bf16, heads of width
+// 2*half, row r at positions[r]; cos/sin [max_len][half] f32.
+hipError_t launch_rope_rows(uint16_t *x, uint32_t rows, uint32_t cols, uint32_t half,
+                            const uint32_t *positions, const float *cos_tab, const float *sin_tab,
+                            hipStream_t stream);
+
+// rope(q) in place + rope(k) and v into the pool over the write plan.
+hipError_t launch_rope_cache(const PoolLayer &pool, uint16_t *q, uint32_t q_cols, uint32_t group,
+                             const uint16_t *keys, const uint16_t *values, const WritePlan &plan,
+                             const uint32_t *positions, const float *cos_tab, const float *sin_tab,
+                             hipStream_t stream);
 
 // reshape_and_cache: pool[slot_mapping[t]] = keys[t], values[t].
 // keys/values: [rows, kv_heads*head_dim] bf16.  Rows whose slot is

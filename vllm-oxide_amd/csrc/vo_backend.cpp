@@ -169,6 +169,9 @@ struct vo_step_meta {
     std::vector<uint32_t> row_num_keys; // [T]
     uint32_t max_block = 0;             // max table entry (0 if none)
     uint32_t max_slot = 0;              // max slot (0 if none)
+    bool has_positions = false;         // positions were uploaded (RoPE needs them)
+    std::vector<uint32_t> positions;    // [T] when uploaded
+    uint32_t max_position = 0;          // largest position (0 if none)
 
     // Device buffer and pinned staging of the same size.
     uint8_t *d_buf = nullptr;
@@ -183,6 +186,7 @@ struct vo_step_meta {
 
     kernels::MetaView view{};
     const uint32_t *d_write_slots = nullptr;  // slots with superseded rows = kSkipSlot
+    kernels::WritePlan write_plan{};          // runs of consecutive slots inside one block
     kernels::DecodePlan plan{};
     bool decode_planned = false;
     std::vector<TailItem> tail_items;  // scratch of plan_decode (capacity kept across steps)
@@ -287,7 +291,7 @@ vo_status check_rows(const char *op, uint64_t num_rows, uint64_t num_seqs, uint6
 vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t block_size,
                         uint64_t num_seqs, const uint64_t *table_off, const uint32_t *tables,
                         uint64_t num_rows, const uint32_t *slot_mapping, const uint64_t *row_seq,
-                        const uint64_t *row_num_keys, Packer &pk) {
+                        const uint64_t *row_num_keys, const uint32_t *positions, Packer &pk) {
     if (block_size == 0) return fail_shape(op, "block_size 0");
     if (num_seqs > m->max_seqs) return fail_capacity("sequences per step", num_seqs, m->max_seqs);
     if (num_rows > m->max_rows) return fail_capacity("tokens per step", num_rows, m->max_rows);
@@ -330,6 +334,20 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     for (uint64_t r = 0; r < num_rows; ++r)
         h[r] = m->row_num_keys[r] = row_num_keys ? static_cast<uint32_t>(row_num_keys[r]) : 0u;
     m->view.row_num_keys = dp;
+    // Positions (RoPE): kept only when the caller gave them.
+    m->has_positions = positions != nullptr || num_rows == 0;
+    m->max_position = 0;
+    m->positions.clear();
+    m->view.positions = nullptr;
+    if (positions) {
+        m->positions.assign(positions, positions + num_rows);
+        h = pk.add(num_rows, &dp);
+        for (uint64_t r = 0; r < num_rows; ++r) {
+            h[r] = positions[r];
+            m->max_position = std::max(m->max_position, positions[r]);
+        }
+        m->view.positions = dp;
+    }
     // Write slots: a slot that appears again later keeps only its last row,
     // the reference's "later row wins" copy order (cpu/mod.rs:277-283).
     h = pk.add(num_rows, &dp);
@@ -347,6 +365,36 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     }
     m->d_write_slots = dp;
     m->view.slot_mapping = dp;
+    // Write plan: maximal runs of rows whose slots are consecutive inside one
+    // block of the pool, as (first row, rows, first slot).  A prefill chunk
+    // becomes whole blocks plus partial ends, a decode step one-row runs.  A
+    // superseded row is a one-row run with slot kSkipSlot: nothing is cached
+    // for it, but the fused RoPE write still rotates its q row.
+    {
+        const uint32_t *ws = h;
+        const uint64_t pbs = m->pool_block_size ? m->pool_block_size : 1;
+        auto run_end = [&](uint64_t r) {
+            uint64_t e = r + 1;
+            if (ws[r] == kSkipSlot) return e;
+            while (e < num_rows && ws[e] != kSkipSlot && ws[e] == ws[e - 1] + 1 && ws[e] % pbs != 0)
+                ++e;
+            return e;
+        };
+        uint64_t nseg = 0;
+        for (uint64_t r = 0; r < num_rows; r = run_end(r)) ++nseg;
+        uint32_t *seg = pk.add(3 * nseg, &dp);
+        uint64_t k = 0;
+        for (uint64_t r = 0; r < num_rows;) {
+            const uint64_t e = run_end(r);
+            seg[3 * k] = static_cast<uint32_t>(r);
+            seg[3 * k + 1] = static_cast<uint32_t>(e - r);
+            seg[3 * k + 2] = ws[r];
+            ++k;
+            r = e;
+        }
+        m->write_plan.segments = dp;
+        m->write_plan.num_segments = static_cast<uint32_t>(nseg);
+    }
     m->view.num_rows = static_cast<uint32_t>(num_rows);
     m->view.num_seqs = static_cast<uint32_t>(num_seqs);
     m->decode_planned = false;
@@ -565,6 +613,8 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
 
     const uint64_t u32s = (max_seqs + 1) + max_table_entries + 3 * max_rows  // offsets, tables, row arrays
                           + max_rows                                         // write slots
+                          + 3 * max_rows                                     // write plan
+                          + max_rows                                         // positions
                           + 2 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
                           + 8 * 64;                                          // alignment slack
@@ -613,7 +663,6 @@ extern "C" int32_t vo_step_meta_upload_prefill(
     const uint64_t *row_seq, const uint64_t *row_num_keys, void *stream) {
     const char *op = "prefill";
     if (!m) return fail_argument(op, "null meta");
-    (void)positions;  // positions feed RoPE, which runs before the cache write
     if (num_seqs && (!context_lens || !seq_row_starts))
         return fail_argument(op, "null context_lens or seq_row_starts");
     if (seq_row_starts && (seq_row_starts[0] != 0 || seq_row_starts[num_seqs] != num_rows))
@@ -624,7 +673,7 @@ extern "C" int32_t vo_step_meta_upload_prefill(
     DeviceGuard guard(m->device);
     Packer pk(m);
     if (vo_status rc = upload_common(m, kPrefill, op, block_size, num_seqs, table_off, tables,
-                                     num_rows, slot_mapping, row_seq, row_num_keys, pk))
+                                     num_rows, slot_mapping, row_seq, row_num_keys, positions, pk))
         return rc;
     if (vo_status rc = plan_prefill(m, pk, context_lens, seq_row_starts)) {
         m->kind = kNone;
@@ -647,11 +696,10 @@ extern "C" int32_t vo_step_meta_upload_decode(vo_step_meta *m, uint64_t block_si
                                               const uint64_t *row_num_keys, void *stream) {
     const char *op = "decode";
     if (!m) return fail_argument(op, "null meta");
-    (void)positions;
     DeviceGuard guard(m->device);
     Packer pk(m);
     if (vo_status rc = upload_common(m, kDecode, op, block_size, num_seqs, table_off, tables,
-                                     num_seqs, slot_mapping, row_seq, row_num_keys, pk))
+                                     num_seqs, slot_mapping, row_seq, row_num_keys, positions, pk))
         return rc;
     if (vo_status rc = plan_decode(m, pk)) {
         m->kind = kNone;
@@ -674,7 +722,7 @@ extern "C" int32_t vo_step_meta_upload_slots(vo_step_meta *m, const uint32_t *sl
     const uint64_t zero = 0;
     Packer pk(m);
     if (vo_status rc = upload_common(m, kSlots, op, m->pool_block_size ? m->pool_block_size : 1, 0,
-                                     &zero, nullptr, num_slots, slots, nullptr, nullptr, pk))
+                                     &zero, nullptr, num_slots, slots, nullptr, nullptr, nullptr, pk))
         return rc;
     if (!pk.fits()) {
         m->kind = kNone;
@@ -748,11 +796,13 @@ vo_status device_status(const char *op, hipError_t err) {
 
 }  // namespace
 
-extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys,
-                               const void *values, uint64_t rows, uint64_t cols,
-                               const vo_step_meta *m, void *stream) {
+namespace {
+
+// write_kv's checks: arena/ops.rs:116-127 (shape), cpu/mod.rs:265-272 (every
+// slot in range before any write).
+vo_status check_write(const vo_kv_pool *pool, uint64_t layer, uint64_t rows, uint64_t cols,
+                      const vo_step_meta *m) {
     const char *op = "write_kv";
-    if (!pool || !m) return fail_argument(op, "null pool or meta");
     const vo_kv_layout &L = pool->layout;
     const uint64_t slot_width = L.kv_heads * L.head_dim;
     // arena/ops.rs:116-127
@@ -763,6 +813,11 @@ extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *key
                                   std::to_string(cols) + "], " + std::to_string(m->num_rows) +
                                   " slots, layer " + std::to_string(layer) + ", pool " +
                                   layout_text(L));
+    // The write plan's runs were cut at the block size of the pool the
+    // metadata was created for.
+    if (m->pool_block_size != L.block_size)
+        return fail_shape(op, "step metadata was created for a pool with block size " +
+                                  std::to_string(m->pool_block_size) + ", pool " + layout_text(L));
     // cpu/mod.rs:265-272: every slot in range before any write.
     const uint64_t num_slots = vo_kv_layout_num_slots(&L);
     if (rows && m->max_slot >= num_slots) {
@@ -779,6 +834,18 @@ extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *key
             }
         }
     }
+    return VO_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys,
+                               const void *values, uint64_t rows, uint64_t cols,
+                               const vo_step_meta *m, void *stream) {
+    const char *op = "write_kv";
+    if (!pool || !m) return fail_argument(op, "null pool or meta");
+    const vo_kv_layout &L = pool->layout;
+    if (vo_status rc = check_write(pool, layer, rows, cols, m)) return rc;
     if (rows == 0) {
         clear_error();
         return VO_OK;
@@ -787,10 +854,205 @@ extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *key
     if (!aligned16(keys) || !aligned16(values))
         return fail_argument(op, "keys and values must be 16-byte aligned");
     DeviceGuard guard(pool->device);
-    hipError_t err = kernels::launch_reshape_and_cache(
-        pool->layer(layer), static_cast<const uint16_t *>(keys),
-        static_cast<const uint16_t *>(values), m->d_write_slots, static_cast<uint32_t>(rows),
+    hipError_t err;
+    if (kernels::cache_write_supported(static_cast<uint32_t>(L.head_dim),
+                                       static_cast<uint32_t>(L.block_size)))
+        err = kernels::launch_cache_write(pool->layer(layer), static_cast<const uint16_t *>(keys),
+                                          static_cast<const uint16_t *>(values), m->write_plan,
+                                          static_cast<hipStream_t>(stream));
+    else
+        err = kernels::launch_reshape_and_cache(
+            pool->layer(layer), static_cast<const uint16_t *>(keys),
+            static_cast<const uint16_t *>(values), m->d_write_slots, static_cast<uint32_t>(rows),
+            static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE
+// ---------------------------------------------------------------------------
+struct vo_rope_table {
+    int device = 0;
+    uint64_t head_dim = 0, half = 0, max_len = 0;
+    float *d_cos = nullptr;  // [max_len][half]
+    float *d_sin = nullptr;
+};
+
+namespace {
+
+// llama3_inv_freq (rope.rs:36-60) and RopeTable::new (rope.rs:62-84): every
+// operation is the reference's f32 operation in its order, with no
+// contraction, and cos/sin/pow come from the host libm as in the reference.
+void rope_host_table(const vo_rope_config &c, uint64_t max_len, std::vector<float> &cos_t,
+                     std::vector<float> &sin_t) {
+#pragma clang fp contract(off)
+    const uint64_t d_i = c.head_dim;
+    const uint64_t half = d_i / 2;
+    const float d = static_cast<float>(d_i);
+    const float base = static_cast<float>(c.rope_theta);
+    const float factor = static_cast<float>(c.factor);
+    const float low = static_cast<float>(c.low_freq_factor);
+    const float high = static_cast<float>(c.high_freq_factor);
+    const float old_ctx = static_cast<float>(c.original_max_position_embeddings);
+    const float low_freq_wavelen = old_ctx / low;
+    const float high_freq_wavelen = old_ctx / high;
+    const float pi = 3.14159265358979323846f;  // std::f32::consts::PI
+    std::vector<float> inv(half);
+    for (uint64_t i = 0; i < half; ++i) {
+        const float raw = 1.0f / powf(base, static_cast<float>(2 * i) / d);
+        const float wavelen = 2.0f * pi / raw;
+        float r;
+        if (wavelen < high_freq_wavelen) {
+            r = raw;
+        } else if (wavelen > low_freq_wavelen) {
+            r = raw / factor;
+        } else {
+            const float smooth = (old_ctx / wavelen - low) / (high - low);
+            r = (1.0f - smooth) * raw / factor + smooth * raw;
+        }
+        inv[i] = r;
+    }
+    cos_t.resize(max_len * half);
+    sin_t.resize(max_len * half);
+    for (uint64_t p = 0; p < max_len; ++p) {
+        for (uint64_t i = 0; i < half; ++i) {
+            const float th = static_cast<float>(p) * inv[i];
+            cos_t[p * half + i] = cosf(th);
+            sin_t[p * half + i] = sinf(th);
+        }
+    }
+}
+
+// cpu/mod.rs:232-247 and arena/ops.rs:86-96 for one operand of rope.
+vo_status check_rope(const char *op, const vo_rope_table *t, uint64_t rows, uint64_t cols,
+                     uint64_t head_dim, const vo_step_meta *m) {
+    const bool shape_ok = m->has_positions && rows == m->num_rows && head_dim > 0 &&
+                          head_dim % 2 == 0 && cols % head_dim == 0;
+    if (!shape_ok)
+        return fail_shape(op, "x [" + std::to_string(rows) + ", " + std::to_string(cols) + "], " +
+                                  (m->has_positions ? std::to_string(m->num_rows) : std::string("no")) +
+                                  " positions, head_dim " + std::to_string(head_dim));
+    if (head_dim != 2 * t->half)
+        return fail_shape(op, "head_dim " + std::to_string(head_dim) + ", table built for " +
+                                  std::to_string(2 * t->half));
+    if (rows && m->max_position >= t->max_len) {
+        // The first position past the table, in row order (cpu/mod.rs:241).
+        uint64_t pos = m->max_position;
+        for (uint32_t p : m->positions) {
+            if (p >= t->max_len) {
+                pos = p;
+                break;
+            }
+        }
+        Error e;
+        e.status = VO_ERR_POSITION_OUT_OF_RANGE;
+        e.op = "rope";
+        e.value = pos;
+        e.limit = t->max_len;
+        e.message = "rope: position " + std::to_string(pos) + " beyond the precomputed table (" +
+                    std::to_string(t->max_len) + ")";
+        return fail(e);
+    }
+    return VO_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t vo_rope_table_create(const vo_rope_config *config, uint64_t max_len,
+                                        int32_t device, vo_rope_table **out) {
+    const char *op = "rope_table_create";
+    if (!config || !out) return fail_argument(op, "null config or output");
+    *out = nullptr;
+    if (config->head_dim == 0 || config->head_dim % 2 != 0 || max_len == 0)
+        return fail_shape(op, "head_dim must be even and non-zero, max_len non-zero");
+    if (max_len > 0xffffffffull) return fail_capacity("rope positions (u32)", max_len, 0xffffffffull);
+    DeviceGuard guard(device);
+    if (!guard.ok()) return fail_device(op, hipErrorInvalidDevice, "hipSetDevice");
+    std::vector<float> cos_t, sin_t;
+    rope_host_table(*config, max_len, cos_t, sin_t);
+    vo_rope_table *t = new (std::nothrow) vo_rope_table();
+    if (!t) return fail_argument(op, "out of host memory");
+    t->device = device;
+    t->head_dim = config->head_dim;
+    t->half = config->head_dim / 2;
+    t->max_len = max_len;
+    const size_t bytes = cos_t.size() * sizeof(float);
+    hipError_t err = hipMalloc(reinterpret_cast<void **>(&t->d_cos), bytes);
+    if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void **>(&t->d_sin), bytes);
+    if (err == hipSuccess) err = hipMemcpy(t->d_cos, cos_t.data(), bytes, hipMemcpyHostToDevice);
+    if (err == hipSuccess) err = hipMemcpy(t->d_sin, sin_t.data(), bytes, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        vo_status rc = fail_device(op, err, hipGetErrorString(err));
+        if (t->d_cos) (void)hipFree(t->d_cos);
+        if (t->d_sin) (void)hipFree(t->d_sin);
+        delete t;
+        return rc;
+    }
+    *out = t;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" void vo_rope_table_destroy(vo_rope_table *t) {
+    if (!t) return;
+    DeviceGuard guard(t->device);
+    (void)hipFree(t->d_cos);
+    (void)hipFree(t->d_sin);
+    delete t;
+}
+
+extern "C" int32_t vo_rope(const vo_rope_table *t, void *x, uint64_t rows, uint64_t cols,
+                           uint64_t head_dim, const vo_step_meta *m, void *stream) {
+    const char *op = "rope";
+    if (!t || !m) return fail_argument(op, "null table or meta");
+    if (vo_status rc = check_rope(op, t, rows, cols, head_dim, m)) return rc;
+    if (rows == 0 || cols == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!x) return fail_argument(op, "null x");
+    if (rows > kU32Limit || cols > kU32Limit) return fail_capacity("rope rows/cols (u32)", std::max(rows, cols), kU32Limit);
+    if (t->half % 8 == 0 && !aligned16(x)) return fail_argument(op, "x must be 16-byte aligned");
+    DeviceGuard guard(t->device);
+    const hipError_t err = kernels::launch_rope_rows(
+        static_cast<uint16_t *>(x), static_cast<uint32_t>(rows), static_cast<uint32_t>(cols),
+        static_cast<uint32_t>(t->half), m->view.positions, t->d_cos, t->d_sin,
         static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_rope_table *t,
+                                    void *queries, uint64_t q_cols, const void *keys,
+                                    const void *values, uint64_t rows, uint64_t kv_cols,
+                                    const vo_step_meta *m, void *stream) {
+    const char *op = "rope_write_kv";
+    if (!pool || !t || !m) return fail_argument(op, "null pool, table or meta");
+    const vo_kv_layout &L = pool->layout;
+    if (vo_status rc = check_rope("rope", t, rows, q_cols, L.head_dim, m)) return rc;
+    if (vo_status rc = check_rope("rope", t, rows, kv_cols, L.head_dim, m)) return rc;
+    if (!kernels::cache_write_supported(static_cast<uint32_t>(L.head_dim),
+                                        static_cast<uint32_t>(L.block_size)))
+        return fail_unsupported(op, "the fused write needs block size 16 and head_dim 64 or 128");
+    // write_kv's checks (arena/ops.rs:116-127, cpu/mod.rs:265-272).
+    if (vo_status rc = check_write(pool, layer, rows, kv_cols, m)) return rc;
+    if (q_cols % (L.kv_heads * L.head_dim) != 0)
+        return fail_shape(op, "q_cols " + std::to_string(q_cols) + " is not a multiple of kv_heads * head_dim");
+    if (rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!queries || !keys || !values) return fail_argument(op, "null queries, keys or values");
+    if (!aligned16(queries) || !aligned16(keys) || !aligned16(values))
+        return fail_argument(op, "queries, keys and values must be 16-byte aligned");
+    if (overlaps(queries, rows * q_cols * 2, keys, rows * kv_cols * 2) ||
+        overlaps(queries, rows * q_cols * 2, values, rows * kv_cols * 2))
+        return fail_shape(op, "queries overlap keys or values");
+    DeviceGuard guard(pool->device);
+    const uint32_t group = static_cast<uint32_t>(q_cols / L.head_dim / L.kv_heads);
+    const hipError_t err = kernels::launch_rope_cache(
+        pool->layer(layer), static_cast<uint16_t *>(queries), static_cast<uint32_t>(q_cols), group,
+        static_cast<const uint16_t *>(keys), static_cast<const uint16_t *>(values), m->write_plan,
+        m->view.positions, t->d_cos, t->d_sin, static_cast<hipStream_t>(stream));
     return device_status(op, err);
 }
 

@@ -225,6 +225,7 @@ extern "C" const char *vo_status_name(int32_t status) {
         case VO_ERR_DEVICE: return "VO_ERR_DEVICE";
         case VO_ERR_INVALID_ARGUMENT: return "VO_ERR_INVALID_ARGUMENT";
         case VO_ERR_UNSUPPORTED: return "VO_ERR_UNSUPPORTED";
+        case VO_ERR_POSITION_OUT_OF_RANGE: return "VO_ERR_POSITION_OUT_OF_RANGE";
         default: return "VO_ERR_UNKNOWN";
     }
 }
