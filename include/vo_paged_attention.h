@@ -286,6 +286,73 @@ int32_t vo_gather_kv(const vo_kv_pool *pool, uint64_t layer, const vo_step_meta 
                      void *stream);
 
 /* ------------------------------------------------------------------ */
+/* KV block manager and prefix cache (host side)                       */
+/* ------------------------------------------------------------------ */
+
+/* No counterpart in the reference snapshot: it plans the block manager (the
+ * owner's M2) and the prefix cache (M4) (README.md:14, CLAUDE.md:26,
+ * docs/process.md:43-47) and fixes their invariant (CLAUDE.md:71): every
+ * block is free or referenced by >= 1 block table, its refcount equals the
+ * number of references, nothing is freed while a sequence uses it.  It
+ * replaces the M0 driver's block counter (generate.rs:4-7).  Host only; it
+ * makes no HIP call.  Block tables it returns feed PrefillSeq / DecodeSeq.
+ *
+ * Prefix caching shares whole blocks: block i of a sequence is identified by
+ * a hash chained over the token ids of blocks 0..i, and a hit also compares
+ * the stored token ids.  A prompt reuses its longest run of cached leading
+ * blocks, never the block holding its last token.  Blocks whose sequences
+ * are all freed stay cached (least recently used first out) until a new
+ * block is needed.  An empty pool is VO_ERR_CAPACITY and changes nothing
+ * (preemption is the scheduler's policy, docs/grill-log.md:86-88). */
+typedef struct vo_block_manager vo_block_manager;
+
+typedef struct vo_bm_stats {
+    uint64_t hit_blocks;          /* prompt blocks served from the prefix cache */
+    uint64_t lookup_blocks;       /* prompt blocks that could have been served */
+    uint64_t evictions;           /* cached idle blocks reused for new contents */
+    uint64_t copies;              /* copy-on-write block copies handed out */
+    uint64_t free_blocks;         /* on the free list now */
+    uint64_t cached_idle_blocks;  /* refcount 0, still cached, now */
+    uint64_t sequences;           /* live sequences now */
+} vo_bm_stats;
+
+int32_t vo_bm_create(uint64_t num_blocks, uint64_t block_size, int32_t prefix_caching,
+                     vo_block_manager **out);
+void vo_bm_destroy(vo_block_manager *bm);
+/* Admits a sequence with its prompt and gives it ceil(n / bs) blocks;
+ * *cached_tokens = prompt tokens whose KV the prefix cache already holds
+ * (a multiple of bs; the step computes the rest). */
+int32_t vo_bm_add_sequence(vo_block_manager *bm, uint64_t seq_id, const uint32_t *tokens,
+                           uint64_t num_tokens, uint64_t *cached_tokens);
+/* Appends one token: a new block on a block boundary; a copy of the last
+ * block when a fork shares it, reported as *copy_src -> *copy_dst (else both
+ * 0xffffffff) for vo_kv_copy_blocks.  *slot is the token's KV slot. */
+int32_t vo_bm_append_token(vo_block_manager *bm, uint64_t seq_id, uint32_t token, uint32_t *slot,
+                           uint32_t *copy_src, uint32_t *copy_dst);
+/* The child shares every block of the parent (one more reference each). */
+int32_t vo_bm_fork(vo_block_manager *bm, uint64_t parent, uint64_t child);
+/* Drops the sequence's references. */
+int32_t vo_bm_free_sequence(vo_block_manager *bm, uint64_t seq_id);
+/* Copies the sequence's block table into out[capacity] (out may be NULL to
+ * query *len); *num_tokens = its token count. */
+int32_t vo_bm_block_table(const vo_block_manager *bm, uint64_t seq_id, uint32_t *out,
+                          uint64_t capacity, uint64_t *len, uint64_t *num_tokens);
+/* Blocks a new sequence could take now (free + cached idle). */
+uint64_t vo_bm_num_available(const vo_block_manager *bm);
+int32_t vo_bm_get_stats(const vo_block_manager *bm, vo_bm_stats *out);
+/* Checks CLAUDE.md:71 and the manager's bookkeeping exhaustively; VO_OK or
+ * VO_ERR_SHAPE with the first violation in vo_last_error's message. */
+int32_t vo_bm_check_invariants(const vo_block_manager *bm);
+
+/* Copies whole blocks of every layer's K and V in the pool: for each i,
+ * block dst[i] := block src[i] (the block manager's copy-on-write).  Block
+ * ids are checked against the pool (VO_ERR_BLOCK_OUT_OF_RANGE); a
+ * destination may not repeat or also be a source (VO_ERR_SHAPE).
+ * Asynchronous on `stream`; the id arrays are host arrays. */
+int32_t vo_kv_copy_blocks(vo_kv_pool *pool, const uint32_t *src, const uint32_t *dst,
+                          uint64_t count, void *stream);
+
+/* ------------------------------------------------------------------ */
 /* Rotary position embedding (Backend::rope, mod.rs:105; rope.rs)      */
 /* ------------------------------------------------------------------ */
 

@@ -629,3 +629,96 @@ def test_rope_write_kv_repeated_slot_rotates_every_q_row(vo, gpu_backend):
     assert np.array_equal(_bits(kc[0:1]).view(np.uint16), k_rot[2:3])
     assert np.array_equal(_bits(kc[1:2]).view(np.uint16), k_rot[1:2])
     assert np.array_equal(_bits(vc[0:1]), _bits(v[2:3]))
+
+
+# ---------------------------------------------------------------------------
+# Block manager + prefix cache feeding the GPU path
+# ---------------------------------------------------------------------------
+def test_copy_blocks_bitwise(vo, gpu_backend):
+    """vo_kv_copy_blocks copies whole blocks of every layer's K and V."""
+    import torch
+    _say("copy_blocks")
+    hd, kvh, bs = 128, 8, 16
+    pool = gpu_backend.alloc_kv_pool(vo.KvLayout(3, 64, bs, kvh, hd))
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(3)
+    slots = np.arange(64 * bs, dtype=np.uint32)
+    k = torch.randn((64 * bs, kvh * hd), generator=g, device="cuda:0").to(torch.bfloat16)
+    v = torch.randn((64 * bs, kvh * hd), generator=g, device="cuda:0").to(torch.bfloat16)
+    for layer in range(3):
+        gpu_backend.write_kv(pool, layer, k, v, slots)
+    pairs = [(5, 40), (6, 41), (63, 0)]
+    gpu_backend.copy_blocks(pool, pairs)
+    for layer in range(3):
+        for src, dst in pairs:
+            a = gpu_backend.read_kv(pool, layer, vo.DecodeMeta.new([vo.DecodeSeq(0, [src])], bs), 0, bs)
+            b = gpu_backend.read_kv(pool, layer, vo.DecodeMeta.new([vo.DecodeSeq(0, [dst])], bs), 0, bs)
+            assert np.array_equal(_bits(a[0]), _bits(b[0])) and np.array_equal(_bits(a[1]), _bits(b[1]))
+    with pytest.raises(vo.BlockOutOfRange):
+        gpu_backend.copy_blocks(pool, [(64, 1)])
+    with pytest.raises(vo.ShapeError):
+        gpu_backend.copy_blocks(pool, [(1, 2), (2, 3)])
+
+
+def test_block_manager_prefix_cache_and_fork_decode(vo, gpu_backend):
+    """The block manager builds a prefix-shared batch (the prefix's KV is
+    written once, by the first sequence), then forks a sequence and appends
+    to both copies (copy on write through vo_kv_copy_blocks).  Decode
+    attention over the manager's tables matches the oracle run on the same
+    KV laid out in private, unshared tables."""
+    import torch
+    _say("block manager -> decode")
+    hd, heads, kvh, bs = 128, 32, 8, 16
+    width = kvh * hd
+    bm = vo.BlockManager(600, bs)
+    pool = gpu_backend.alloc_kv_pool(vo.KvLayout(1, 600, bs, kvh, hd))
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(11)
+    rnd = lambda n: torch.randn((n, width), generator=g, device="cuda:0").to(torch.bfloat16)
+    prefix = list(range(1000))
+    kv = {}          # seq -> (k, v) for every position, host f32 (what the oracle reads)
+    prompts = {s: prefix + [2000 + s] * (37 * s + 5) for s in range(6)}
+    prefix_kv = (rnd(1000), rnd(1000))
+    for s, toks in prompts.items():
+        cached = bm.add_sequence(s, toks)
+        assert cached == (0 if s == 0 else 992)
+        table = bm.block_table(s)
+        n = len(toks)
+        k_all = torch.cat([prefix_kv[0], rnd(n - 1000)])
+        v_all = torch.cat([prefix_kv[1], rnd(n - 1000)])
+        lo = cached
+        slots = np.array([table[p // bs] * bs + p % bs for p in range(lo, n)], np.uint32)
+        gpu_backend.write_kv(pool, 0, k_all[lo:].contiguous(), v_all[lo:].contiguous(), slots)
+        kv[s] = [k_all, v_all]
+    # fork sequence 3 and append one token to each copy
+    bm.fork(3, 9)
+    kv[9] = [t.clone() for t in kv[3]]
+    for s in (3, 9):
+        slot, copy = bm.append_token(s, 7)
+        if copy is not None:
+            gpu_backend.copy_blocks(pool, [copy])
+        kn, vn = rnd(1), rnd(1)
+        gpu_backend.write_kv(pool, 0, kn, vn, np.array([slot], np.uint32))
+        kv[s][0] = torch.cat([kv[s][0], kn])
+        kv[s][1] = torch.cat([kv[s][1], vn])
+    bm.check()
+    seqs = sorted(kv)
+    tables = [bm.block_table(s) for s in seqs]
+    ctx = [bm.num_tokens(s) - 1 for s in seqs]
+    meta = vo.DecodeMeta.new([vo.DecodeSeq(c, t) for c, t in zip(ctx, tables)], bs)
+    q = torch.randn((len(seqs), heads * hd), generator=g, device="cuda:0").to(torch.bfloat16)
+    out = gpu_backend.decode_attention(q, pool, 0, meta).float().cpu().numpy()
+    # oracle: each sequence's keys in private consecutive blocks
+    opool = orc.Pool(1, 2000, bs, kvh, hd)
+    otables, base = [], 0
+    for s in seqs:
+        n = kv[s][0].shape[0]
+        nb = -(-n // bs)
+        t = np.arange(base, base + nb, dtype=np.uint32)
+        base += nb
+        otables.append(t)
+        opool.write_kv(0, kv[s][0].float().cpu().numpy(), kv[s][1].float().cpu().numpy(),
+                       [int(t[p // bs]) * bs + p % bs for p in range(n)])
+    want = opool.attention(q.float().cpu().numpy(), 0, otables, np.arange(len(seqs)),
+                           np.asarray(ctx) + 1)
+    _assert_close(out, want, "block manager decode")

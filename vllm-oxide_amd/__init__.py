@@ -81,6 +81,12 @@ class vo_rope_config(ctypes.Structure):
                 ("original_max_position_embeddings", _u64)]
 
 
+class vo_bm_stats(ctypes.Structure):
+    _fields_ = [("hit_blocks", _u64), ("lookup_blocks", _u64), ("evictions", _u64),
+                ("copies", _u64), ("free_blocks", _u64), ("cached_idle_blocks", _u64),
+                ("sequences", _u64)]
+
+
 class vo_prefill_seq(ctypes.Structure):
     _fields_ = [("context_len", _u64), ("num_new", _u64), ("block_table", _u32p),
                 ("block_table_len", _u64)]
@@ -122,6 +128,17 @@ SIGNATURES = {
     "vo_gather_kv": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _vp, _vp, _vp]),
     "vo_prefill_meta_build_device": (ctypes.c_int32, [_vp, _vp, _vp, _vp, _u64, _u64, _u64,
                                                       _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vo_bm_create": (ctypes.c_int32, [_u64, _u64, ctypes.c_int32, ctypes.POINTER(_vp)]),
+    "vo_bm_destroy": (None, [_vp]),
+    "vo_bm_add_sequence": (ctypes.c_int32, [_vp, _u64, _u32p, _u64, _u64p]),
+    "vo_bm_append_token": (ctypes.c_int32, [_vp, _u64, ctypes.c_uint32, _u32p, _u32p, _u32p]),
+    "vo_bm_fork": (ctypes.c_int32, [_vp, _u64, _u64]),
+    "vo_bm_free_sequence": (ctypes.c_int32, [_vp, _u64]),
+    "vo_bm_block_table": (ctypes.c_int32, [_vp, _u64, _u32p, _u64, _u64p, _u64p]),
+    "vo_bm_num_available": (_u64, [_vp]),
+    "vo_bm_get_stats": (ctypes.c_int32, [_vp, ctypes.POINTER(vo_bm_stats)]),
+    "vo_bm_check_invariants": (ctypes.c_int32, [_vp]),
+    "vo_kv_copy_blocks": (ctypes.c_int32, [_vp, _u32p, _u32p, _u64, _vp]),
     "vo_rope_table_create": (ctypes.c_int32, [ctypes.POINTER(vo_rope_config), _u64,
                                               ctypes.c_int32, ctypes.POINTER(_vp)]),
     "vo_rope_table_destroy": (None, [_vp]),
@@ -503,6 +520,75 @@ def _dev_ptr(t) -> _vp:
     return _vp(t.data_ptr())
 
 
+class BlockManager:
+    """KV block manager with refcounted blocks and a full-block prefix cache
+    (the reference's planned M2/M4 components; invariant CLAUDE.md:71).
+    Host only: no GPU needed."""
+
+    NONE = 0xFFFFFFFF
+
+    def __init__(self, num_blocks: int, block_size: int, prefix_caching: bool = True):
+        self._h = _vp()
+        _check(lib.vo_bm_create(num_blocks, block_size, int(prefix_caching), ctypes.byref(self._h)))
+        self.num_blocks, self.block_size = num_blocks, block_size
+
+    def add_sequence(self, seq_id: int, tokens) -> int:
+        """Admit a sequence with its prompt; returns the prompt tokens already cached."""
+        t = _u32(tokens) if len(tokens) else np.zeros(1, np.uint32)
+        cached = ctypes.c_uint64(0)
+        _check(lib.vo_bm_add_sequence(self._h, seq_id, _p32(t), len(tokens), ctypes.byref(cached)))
+        return cached.value
+
+    def append_token(self, seq_id: int, token: int):
+        """Returns (slot, copy) with copy = (src, dst) block ids or None."""
+        slot, src, dst = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        _check(lib.vo_bm_append_token(self._h, seq_id, token, ctypes.byref(slot),
+                                      ctypes.byref(src), ctypes.byref(dst)))
+        return slot.value, (None if src.value == self.NONE else (src.value, dst.value))
+
+    def fork(self, parent: int, child: int) -> None:
+        _check(lib.vo_bm_fork(self._h, parent, child))
+
+    def free(self, seq_id: int) -> None:
+        _check(lib.vo_bm_free_sequence(self._h, seq_id))
+
+    def block_table(self, seq_id: int) -> np.ndarray:
+        n, toks = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib.vo_bm_block_table(self._h, seq_id, None, 0, ctypes.byref(n), ctypes.byref(toks)))
+        out = np.zeros(max(n.value, 1), np.uint32)
+        _check(lib.vo_bm_block_table(self._h, seq_id, _p32(out), len(out), ctypes.byref(n),
+                                     ctypes.byref(toks)))
+        return out[:n.value]
+
+    def num_tokens(self, seq_id: int) -> int:
+        n, toks = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib.vo_bm_block_table(self._h, seq_id, None, 0, ctypes.byref(n), ctypes.byref(toks)))
+        return toks.value
+
+    def available(self) -> int:
+        return int(lib.vo_bm_num_available(self._h))
+
+    def stats(self) -> dict:
+        st = vo_bm_stats()
+        _check(lib.vo_bm_get_stats(self._h, ctypes.byref(st)))
+        return {f: int(getattr(st, f)) for f, _ in vo_bm_stats._fields_}
+
+    def check(self) -> None:
+        """Raises ShapeError with the first violated invariant."""
+        _check(lib.vo_bm_check_invariants(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_bm_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class RopeTable:
     """RopeTable (rope.rs:24-100) on one device: Llama 3 scaled frequencies,
     cos/sin for positions 0 .. max_len-1.  Defaults are LLAMA_3_2_1B's
@@ -599,6 +685,15 @@ class HipBackend:
         _check(fn(_dev_ptr(queries), queries.shape[0], queries.shape[1], pool.handle, layer,
                   m.handle, _dev_ptr(out), _stream_ptr(stream)))
         return out
+
+    def copy_blocks(self, pool: KvPool, pairs, stream=None) -> None:
+        """Block copies of every layer: pairs = [(src, dst), ...] (copy on write)."""
+        if not pairs:
+            return
+        src = _u32([p[0] for p in pairs])
+        dst = _u32([p[1] for p in pairs])
+        _check(lib.vo_kv_copy_blocks(pool.handle, _p32(src), _p32(dst), len(pairs),
+                                     _stream_ptr(stream)))
 
     # mod.rs:105
     def rope(self, table: RopeTable, x, pool: KvPool, meta, head_dim: int, stream=None) -> None:

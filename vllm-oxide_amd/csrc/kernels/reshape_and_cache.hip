@@ -147,6 +147,23 @@ __global__ __launch_bounds__(256) void cache_write_kernel(
     }
 }
 
+// Block copies of every layer (the block manager's copy on write): workgroup
+// (pair, layer, K|V) copies one block's tiles of all KV heads, which are
+// contiguous in each layer's region, with 16-byte loads and stores.
+__global__ __launch_bounds__(256) void copy_blocks_kernel(uint16_t *__restrict__ base,
+                                                          uint64_t layer_elems,
+                                                          uint64_t block_elems,
+                                                          BlockPairs pairs) {
+    const uint32_t pair = blockIdx.x;
+    const uint32_t layer = blockIdx.y >> 1;
+    const uint32_t which = blockIdx.y & 1;  // 0 = K, 1 = V
+    uint16_t *region = base + (static_cast<uint64_t>(layer) * 2 + which) * layer_elems;
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(region + pairs.src[pair] * block_elems);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(region + pairs.dst[pair] * block_elems);
+    const uint64_t n = block_elems / 8;
+    for (uint64_t i = threadIdx.x; i < n; i += 256) dst[i] = src[i];
+}
+
 __global__ void gather_kv_kernel(const uint16_t *__restrict__ k_pool,
                                  const uint16_t *__restrict__ v_pool, PoolDims dims,
                                  const uint32_t *__restrict__ table, uint32_t num_keys,
@@ -215,6 +232,18 @@ hipError_t launch_cache_write(const PoolLayer &pool, const uint16_t *keys, const
         hipLaunchKernelGGL((cache_write_kernel<64>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
                            stream, pool.k, pool.v, pool.kv_heads, keys, values, plan.segments,
                            static_cast<uint32_t>(items));
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_blocks(uint16_t *base, uint64_t num_layers, uint64_t layer_elems,
+                              uint64_t block_elems, const BlockPairs &pairs, uint32_t count,
+                              hipStream_t stream) {
+    if (count == 0) return hipSuccess;
+    if (count > kMaxBlockPairs || block_elems % 8 != 0 || num_layers * 2 > 65535)
+        return hipErrorInvalidValue;
+    KernelTimer timer("copy_blocks", stream);
+    hipLaunchKernelGGL(copy_blocks_kernel, dim3(count, static_cast<uint32_t>(num_layers * 2)),
+                       dim3(256), 0, stream, base, layer_elems, block_elems, pairs);
     return hipGetLastError();
 }
 

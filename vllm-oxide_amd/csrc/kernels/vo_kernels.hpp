@@ -84,6 +84,19 @@ hipError_t launch_reshape_and_cache(const PoolLayer &pool, const uint16_t *keys,
                                     const uint16_t *values, const uint32_t *slot_mapping,
                                     uint32_t rows, hipStream_t stream);
 
+// Up to kMaxBlockPairs (src, dst) block pairs, passed by value.
+constexpr uint32_t kMaxBlockPairs = 128;
+struct BlockPairs {
+    uint32_t src[kMaxBlockPairs];
+    uint32_t dst[kMaxBlockPairs];
+};
+
+// dst[i] := src[i] for whole blocks of every layer's K and V.  base is the
+// pool's [layers][K|V][layer_elems]; block_elems = kv_heads*block_size*head_dim.
+hipError_t launch_copy_blocks(uint16_t *base, uint64_t num_layers, uint64_t layer_elems,
+                              uint64_t block_elems, const BlockPairs &pairs, uint32_t count,
+                              hipStream_t stream);
+
 // Gather keys 0..num_keys of one sequence, whose block table is the device
 // array `table`, into [num_keys, kv_heads*head_dim] (the reference's layout).
 hipError_t launch_gather_kv(const PoolLayer &pool, const uint32_t *table, uint32_t num_keys,

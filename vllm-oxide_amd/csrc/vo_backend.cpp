@@ -1152,6 +1152,51 @@ extern "C" int32_t vo_prefill_meta_build_device(
     return device_status(op, err);
 }
 
+extern "C" int32_t vo_kv_copy_blocks(vo_kv_pool *pool, const uint32_t *src, const uint32_t *dst,
+                                     uint64_t count, void *stream) {
+    const char *op = "copy_blocks";
+    if (!pool) return fail_argument(op, "null pool");
+    if (count == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!src || !dst) return fail_argument(op, "null block ids");
+    const vo_kv_layout &L = pool->layout;
+    std::vector<uint8_t> is_dst(L.num_blocks, 0);
+    for (uint64_t i = 0; i < count; ++i) {
+        for (uint32_t b : {src[i], dst[i]}) {
+            if (b >= L.num_blocks) {
+                Error e;
+                e.status = VO_ERR_BLOCK_OUT_OF_RANGE;
+                e.op = op;
+                e.value = b;
+                e.limit = L.num_blocks;
+                e.message = std::string(op) + ": block " + std::to_string(b) +
+                            " out of range (pool has " + std::to_string(L.num_blocks) + ")";
+                return fail(e);
+            }
+        }
+        if (is_dst[dst[i]]) return fail_shape(op, "block " + std::to_string(dst[i]) + " is a destination twice");
+        is_dst[dst[i]] = 1;
+    }
+    for (uint64_t i = 0; i < count; ++i)
+        if (is_dst[src[i]]) return fail_shape(op, "block " + std::to_string(src[i]) + " is both a source and a destination");
+    DeviceGuard guard(pool->device);
+    const uint64_t block_elems = L.kv_heads * L.block_size * L.head_dim;
+    hipError_t err = hipSuccess;
+    for (uint64_t i0 = 0; i0 < count && err == hipSuccess; i0 += kernels::kMaxBlockPairs) {
+        kernels::BlockPairs pairs{};
+        const uint32_t n = static_cast<uint32_t>(std::min<uint64_t>(kernels::kMaxBlockPairs, count - i0));
+        for (uint32_t j = 0; j < n; ++j) {
+            pairs.src[j] = src[i0 + j];
+            pairs.dst[j] = dst[i0 + j];
+        }
+        err = kernels::launch_copy_blocks(pool->base, L.num_layers, pool->layer_elems, block_elems,
+                                          pairs, n, static_cast<hipStream_t>(stream));
+    }
+    return device_status(op, err);
+}
+
 extern "C" int32_t vo_gather_kv(const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *m,
                                 uint64_t seq, uint64_t num_keys, void *out_keys,
                                 void *out_values, void *stream) {
