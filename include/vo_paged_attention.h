@@ -66,7 +66,8 @@ typedef enum vo_status {
     VO_ERR_DEVICE = 6,                 /* HIP runtime failure (no reference counterpart) */
     VO_ERR_INVALID_ARGUMENT = 7,       /* NULL pointer or zero size where one is required */
     VO_ERR_UNSUPPORTED = 8,            /* shape outside what the kernels are built for */
-    VO_ERR_POSITION_OUT_OF_RANGE = 9   /* EngineError::PositionOutOfRange error.rs:52-53 */
+    VO_ERR_POSITION_OUT_OF_RANGE = 9,  /* EngineError::PositionOutOfRange error.rs:52-53 */
+    VO_ERR_NAN = 10                    /* EngineError::NaN              error.rs:54-55 */
 } vo_status;
 
 /* Detail of the last failed call on the calling thread.  The numeric fields
@@ -400,6 +401,97 @@ int32_t vo_rope(const vo_rope_table *table, void *x, uint64_t rows, uint64_t col
 int32_t vo_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_rope_table *table,
                          void *queries, uint64_t q_cols, const void *keys, const void *values,
                          uint64_t rows, uint64_t kv_cols, const vo_step_meta *meta, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* The rest of the layer (Llama::forward, model.rs:269-356)            */
+/* ------------------------------------------------------------------ */
+
+/* Element type of an activation buffer. */
+typedef enum vo_dtype { VO_DTYPE_BF16 = 0, VO_DTYPE_F32 = 1 } vo_dtype;
+
+/* The step's token ids (Llama::prefill / decode `tokens`, model.rs:221-243),
+ * kept apart from the attention metadata: a host copy for embed's check and
+ * a device copy (one async copy from pinned staging on `stream`).  At most
+ * max_rows ids (VO_ERR_CAPACITY). */
+int32_t vo_step_meta_upload_tokens(vo_step_meta *meta, const uint32_t *tokens,
+                                   uint64_t num_tokens, void *stream);
+
+/* Backend::embed (mod.rs:84; cpu/mod.rs:172-180): row r of out [rows,
+ * hidden] f32 = row tokens[r] of table [vocab, hidden] bf16 (widened, exact),
+ * tokens being the meta's last upload_tokens.  Checks (arena/ops.rs:30-44):
+ * rows == number of tokens, then the first token >= vocab fails with
+ * VO_ERR_SHAPE "embed: token {t} >= vocab {v}". */
+int32_t vo_embed(const void *table, uint64_t vocab, uint64_t hidden, const vo_step_meta *meta,
+                 uint64_t rows, float *out, void *stream);
+
+/* Backend::rmsnorm (mod.rs:91-96; cpu/mod.rs:182-197): out [rows, cols] bf16 =
+ * weight * (x * 1/sqrt(mean(x^2) + eps)) per row, x [rows, cols] f32 (the
+ * residual stream), weight [weight_len] bf16.  Check (arena/ops.rs:47-62):
+ * weight_len == cols (VO_ERR_SHAPE). */
+int32_t vo_rmsnorm(const float *x, uint64_t rows, uint64_t cols, const void *weight,
+                   uint64_t weight_len, float eps, void *out, void *stream);
+
+/* The LM head's input (model.rs:334-343): gather_rows(x, meta.last_rows())
+ * then rmsnorm, in one pass.  out [num_seqs, cols] bf16: row s normalises
+ * the last row of sequence s (PrefillMeta::last_rows, paged.rs:153-159); for
+ * a decode upload every row.  Checks: weight_len == cols, rows == the meta's
+ * rows, and the upload is a prefill or decode one whose sequences all have
+ * rows (VO_ERR_SHAPE). */
+int32_t vo_rmsnorm_last_rows(const float *x, uint64_t rows, uint64_t cols, const void *weight,
+                             uint64_t weight_len, float eps, const vo_step_meta *meta, void *out,
+                             void *stream);
+
+/* Backend::add (mod.rs:161; cpu/mod.rs:351-358): sum [rows, cols] f32 += x
+ * [rows, cols] of x_dtype.  The model's residual adds also run fused into
+ * vo_matmul (accumulate = 1). */
+int32_t vo_add(float *sum, const void *x, int32_t x_dtype, uint64_t rows, uint64_t cols,
+               void *stream);
+
+/* Backend::silu_mul (mod.rs:155; cpu/mod.rs:341-349): out = silu(gate) * up
+ * = gate / (1 + e^-gate) * up, all [rows, cols] bf16 with row strides (in
+ * elements) gate_ld, up_ld, out_ld >= cols.  out may be gate itself (the
+ * reference's in-place form); gate and up may be the two halves of one
+ * fused gate/up projection ([rows, 2*cols], gate_ld = up_ld = 2*cols). */
+int32_t vo_silu_mul(const void *gate, uint64_t gate_ld, const void *up, uint64_t up_ld,
+                    uint64_t rows, uint64_t cols, void *out, uint64_t out_ld, void *stream);
+
+/* Backend::argmax (mod.rs:175; cpu/mod.rs:370-388): ids[r] = index of the
+ * first maximum of row r of logits [rows, cols] (dtype bf16 or f32).  ids is
+ * a device array [rows]; a row with a NaN gets 0xffffffff.  With host_ids
+ * non-NULL the call also copies the ids there, waits for `stream`, and
+ * returns VO_ERR_NAN {op "argmax"} if a row held a NaN -- the step's one
+ * device-to-host synchronisation, as in the reference (arena/ops.rs:252-253). */
+int32_t vo_argmax(const void *logits, int32_t dtype, uint64_t rows, uint64_t cols, uint32_t *ids,
+                  uint32_t *host_ids, void *stream);
+
+/* The layer's "q, k, v = matmul(...); rope(q); rope(k); write_kv(k, v)"
+ * (model.rs:303-311) over one fused QKV projection output: qkv [rows,
+ * q_cols + 2*kv_cols] bf16, each row [q | k | v].  Writes rotated q to q_out
+ * [rows, q_cols] (a contiguous operand for attention), rotates k and writes
+ * k and v to the pool at the meta's slots, in one launch.  Checks and limits
+ * are vo_rope_write_kv's. */
+int32_t vo_qkv_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_rope_table *table,
+                             const void *qkv, uint64_t rows, uint64_t q_cols, uint64_t kv_cols,
+                             const vo_step_meta *meta, void *q_out, void *stream);
+
+/* Dense projections: Backend::matmul (mod.rs:98; cpu/mod.rs:199-229) on
+ * hipBLASLt.  Opaque: one hipBLASLt handle, a workspace and a cache of
+ * per-shape algorithm choices on one device.  hipBLASLt is loaded at
+ * vo_gemm_create (the copy the process already has, else libhipblaslt.so.1);
+ * VO_ERR_UNSUPPORTED when it cannot be. */
+typedef struct vo_gemm vo_gemm;
+int32_t vo_gemm_create(int32_t device, uint64_t workspace_bytes, vo_gemm **out);
+void vo_gemm_destroy(vo_gemm *gemm);
+
+/* out [rows, out_features] = x [rows, x_cols] . weight^T, weight [out_features,
+ * in_features] bf16 (the reference's Weight layout), x bf16, fp32
+ * accumulation, out of out_dtype.  accumulate = 1: out += x . weight^T (the
+ * model's add(residual, matmul(..)), model.rs:320-321 and :330-331, fused
+ * into the GEMM's epilogue).  Check (arena/ops.rs:65-81): in_features ==
+ * x_cols (VO_ERR_SHAPE "x [r, c], weight [o, i]"). */
+int32_t vo_matmul(vo_gemm *gemm, const void *x, uint64_t rows, uint64_t x_cols, const void *weight,
+                  uint64_t out_features, uint64_t in_features, void *out, int32_t out_dtype,
+                  int32_t accumulate, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Opt-in kernel timing (the reference's opt-in per-op timing,         */

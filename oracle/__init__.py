@@ -40,6 +40,7 @@ OK = 0
 BLOCK_TABLE_TOO_SHORT = 3
 SLOT_OUT_OF_RANGE = 4
 BLOCK_OUT_OF_RANGE = 5
+NAN = 10
 
 
 class Err(ctypes.Structure):
@@ -86,6 +87,13 @@ def _load():
                                            ctypes.c_double, ctypes.c_double, _u64, _f32p]),
         "vo_oracle_rope_table": (None, [_f32p, _u64, _u64, _f32p, _f32p]),
         "vo_oracle_rope_apply": (None, [_f32p, _u64, _u64, _u32p, _f32p, _f32p, _u64]),
+        "vo_oracle_embed": (None, [_f32p, _u64, _u32p, _u64, _f32p]),
+        "vo_oracle_rmsnorm": (None, [_f32p, _u64, _u64, _f32p, ctypes.c_float, _f32p]),
+        "vo_oracle_matmul": (None, [_f32p, _u64, _u64, _f32p, _u64, _f32p, ctypes.c_int]),
+        "vo_oracle_silu_mul": (None, [_f32p, _f32p, _u64]),
+        "vo_oracle_add": (None, [_f32p, _f32p, _u64]),
+        "vo_oracle_gather_rows": (None, [_f32p, _u64, _u32p, _u64, _f32p]),
+        "vo_oracle_argmax": (ctypes.c_int, [_f32p, _u64, _u64, _u32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(h, name)
@@ -316,3 +324,154 @@ def rope_apply(x, positions, cos_tab, sin_tab) -> np.ndarray:
     lib.vo_oracle_rope_apply(_pf(x), x.shape[0], x.shape[1], _p32(pos), _pf(c), _pf(sn),
                              c.shape[1])
     return x
+
+
+# ---- cpu/mod.rs: the layer around attention -----------------------------------
+
+def embed(table, tokens) -> np.ndarray:
+    """cpu/mod.rs:172-180."""
+    t, ids = _f32(table), _u32(tokens)
+    out = np.zeros((len(ids), t.shape[1]), np.float32)
+    if len(ids):
+        lib.vo_oracle_embed(_pf(t), t.shape[1], _p32(ids), len(ids), _pf(out))
+    return out
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    """cpu/mod.rs:182-197."""
+    x, w = _f32(x), _f32(w)
+    out = np.zeros_like(x)
+    if x.size:
+        lib.vo_oracle_rmsnorm(_pf(x), x.shape[0], x.shape[1], _pf(w), eps, _pf(out))
+    return out
+
+
+def matmul(x, w, threads=None) -> np.ndarray:
+    """cpu/mod.rs:199-229: x [rows, in] . w[out, in]^T, each element the 16-lane dot."""
+    x, w = _f32(x), _f32(w)
+    out = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    if threads is None:
+        threads = min(os.cpu_count() or 1, 64)
+    if out.size:
+        lib.vo_oracle_matmul(_pf(x), x.shape[0], x.shape[1], _pf(w), w.shape[0], _pf(out),
+                             int(threads))
+    return out
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """cpu/mod.rs:341-349, on a copy of gate."""
+    g, u = _f32(gate).copy(), _f32(up)
+    lib.vo_oracle_silu_mul(_pf(g), _pf(u), g.size)
+    return g
+
+
+def add(total, x) -> np.ndarray:
+    """cpu/mod.rs:351-358, on a copy of total."""
+    s, v = _f32(total).copy(), _f32(x)
+    lib.vo_oracle_add(_pf(s), _pf(v), s.size)
+    return s
+
+
+def gather_rows(x, rows) -> np.ndarray:
+    """cpu/mod.rs:360-368."""
+    x, r = _f32(x), _u32(rows)
+    out = np.zeros((len(r), x.shape[1]), np.float32)
+    if len(r):
+        lib.vo_oracle_gather_rows(_pf(x), x.shape[1], _p32(r), len(r), _pf(out))
+    return out
+
+
+def argmax(x) -> np.ndarray:
+    """cpu/mod.rs:370-388; raises OracleError(NAN) on a NaN."""
+    x = _f32(x)
+    out = np.zeros(max(x.shape[0], 1), np.uint32)
+    rc = lib.vo_oracle_argmax(_pf(x), x.shape[0], x.shape[1], _p32(out))
+    if rc != OK:
+        raise OracleError(rc, Err())
+    return out[:x.shape[0] if x.shape[1] else 0]
+
+
+# ---- testutil.rs: random_weights ------------------------------------------------
+
+def rand_weight(seed: int, shape, scale: float) -> np.ndarray:
+    """testutil.rs:46-53: rand_vec(seed, n) * scale, in f32."""
+    n = int(np.prod(shape))
+    return (rand_vec(seed, n) * np.float32(scale)).astype(np.float32).reshape(shape)
+
+
+def random_weights(cfg, seed: int) -> dict:
+    """testutil.rs:57-91: matrices ~U[-1,1)/sqrt(in), norms 1 + 0.1 U[-1,1).
+    ``cfg`` has the ModelConfig fields (config.rs:9-22) and ``head_dim``."""
+    h, hd = cfg.hidden_size, cfg.head_dim
+    qd, kvd, ffn = cfg.num_attention_heads * hd, cfg.num_key_value_heads * hd, cfg.intermediate_size
+
+    def m(s, o, i):
+        return rand_weight(seed * 1000 + s, (o, i), np.float32(1.0) / np.sqrt(np.float32(i)))
+
+    def norm(s):
+        return (np.float32(1.0) + np.float32(0.1) * rand_vec(seed * 1000 + s, h)).astype(np.float32)
+
+    layers = []
+    for l in range(cfg.num_hidden_layers):
+        b = 10 + l * 10
+        layers.append(dict(attn_norm=norm(b), wq=m(b + 1, qd, h), wk=m(b + 2, kvd, h),
+                           wv=m(b + 3, kvd, h), wo=m(b + 4, h, qd), mlp_norm=norm(b + 5),
+                           w_gate=m(b + 6, ffn, h), w_up=m(b + 7, ffn, h),
+                           w_down=m(b + 8, h, ffn)))
+    return dict(embed=rand_weight(seed * 1000, (cfg.vocab_size, h), 1.0), layers=layers,
+                final_norm=norm(999))
+
+
+# ---- model.rs: Llama::forward ------------------------------------------------------
+
+class Llama:
+    """Llama<CpuBackend> (model.rs:269-356) on the oracle's ops: f32 weights
+    (dict as random_weights returns), f32 KV pool, RoPE table of max_len rows
+    (CpuBackend::new builds it for max_model_len, cpu/mod.rs:53)."""
+
+    def __init__(self, cfg, weights: dict, num_blocks: int, block_size: int, max_len: int,
+                 threads=None):
+        self.cfg, self.w, self.threads = cfg, weights, threads
+        hd = cfg.head_dim
+        self.pool = Pool(cfg.num_hidden_layers, num_blocks, block_size,
+                         cfg.num_key_value_heads, hd)
+        inv = rope_inv_freq(hd, cfg.rope_theta, **cfg.rope_scaling)
+        self.cos, self.sin = rope_table(inv, max_len)
+
+    def forward(self, tokens, positions, slots, tables, row_seq, row_num_keys, last_rows=None):
+        """One step.  ``last_rows`` None: decode (every row feeds the LM head).
+        Returns (next token ids, logits [S, vocab])."""
+        cfg, W = self.cfg, self.w
+        eps = np.float32(cfg.rms_norm_eps)
+        hd = cfg.head_dim
+        residual = embed(W["embed"], tokens)
+        for li, L in enumerate(W["layers"]):
+            normed = rmsnorm(residual, L["attn_norm"], eps)
+            q = matmul(normed, L["wq"], self.threads)
+            k = matmul(normed, L["wk"], self.threads)
+            v = matmul(normed, L["wv"], self.threads)
+            q = rope_apply(q, positions, self.cos, self.sin)
+            k = rope_apply(k, positions, self.cos, self.sin)
+            self.pool.write_kv(li, k, v, slots)
+            attn = self.pool.attention(q, li, tables, row_seq, row_num_keys, self.threads)
+            residual = add(residual, matmul(attn, L["wo"], self.threads))
+            normed = rmsnorm(residual, L["mlp_norm"], eps)
+            gate = matmul(normed, L["w_gate"], self.threads)
+            up = matmul(normed, L["w_up"], self.threads)
+            residual = add(residual, matmul(silu_mul(gate, up), L["w_down"], self.threads))
+        last = residual if last_rows is None else gather_rows(residual, last_rows)
+        normed = rmsnorm(last, W["final_norm"], eps)
+        logits = matmul(normed, W["embed"], self.threads)
+        return argmax(logits), logits
+
+    def prefill(self, tokens, seqs, block_size: int):
+        """seqs = [(context_len, num_new, table)] (PrefillSeq, paged.rs:84-92)."""
+        m = prefill_meta(seqs, block_size)
+        return self.forward(tokens, m["positions"], m["slot_mapping"], [s[2] for s in seqs],
+                            m["row_seq"], m["row_num_keys"], m["last_rows"])
+
+    def decode(self, tokens, seqs, block_size: int):
+        """seqs = [(context_len, table)] (DecodeSeq, paged.rs:164-168)."""
+        m = decode_meta(seqs, block_size)
+        return self.forward(tokens, m["positions"], m["slot_mapping"], [s[1] for s in seqs],
+                            m["row_seq"], m["row_num_keys"], None)

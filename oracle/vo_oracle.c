@@ -13,6 +13,8 @@
  *                             check_block_tables
  *   backend/cpu/tests.rs  naive_attend (the reference's f64 test oracle)
  *   backend/cpu/rope.rs   llama3_inv_freq, RopeTable::new / apply
+ *   backend/cpu/mod.rs    embed, rmsnorm, matmul, silu_mul, add, gather_rows,
+ *                         argmax (the layer around attention)
  */
 #include "vo_oracle.h"
 
@@ -426,4 +428,101 @@ void vo_oracle_rope_apply(float *x, uint64_t rows, uint64_t cols, const uint32_t
             }
         }
     }
+}
+
+/* ---- the rest of the layer: backend/cpu/mod.rs ---------------------- */
+
+/* cpu/mod.rs:172-180. */
+void vo_oracle_embed(const float *table, uint64_t hidden, const uint32_t *tokens, uint64_t rows,
+                     float *out) {
+    for (uint64_t r = 0; r < rows; ++r)
+        memcpy(out + r * hidden, table + (uint64_t)tokens[r] * hidden, hidden * sizeof(float));
+}
+
+/* cpu/mod.rs:182-197.  `dot(x_row, x_row) / hidden as f32`, then
+ * `1.0 / (mean_square + eps).sqrt()`, then `w * (x * inv_rms)`. */
+void vo_oracle_rmsnorm(const float *x, uint64_t rows, uint64_t hidden, const float *w, float eps,
+                       float *out) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        const float *xr = x + r * hidden;
+        float *o = out + r * hidden;
+        float mean_square = vo_oracle_dot(xr, xr, hidden) / (float)hidden;
+        float inv_rms = 1.0f / sqrtf(mean_square + eps);
+        for (uint64_t j = 0; j < hidden; ++j) o[j] = w[j] * (xr[j] * inv_rms);
+    }
+}
+
+typedef struct {
+    const float *x, *w;
+    float *out;
+    uint64_t rows, in, out_f, o_begin, o_end;
+} matmul_job;
+
+static void *matmul_worker(void *arg) {
+    const matmul_job *j = (const matmul_job *)arg;
+    for (uint64_t o = j->o_begin; o < j->o_end; ++o) {
+        const float *wr = j->w + o * j->in;
+        for (uint64_t r = 0; r < j->rows; ++r)
+            j->out[r * j->out_f + o] = vo_oracle_dot(j->x + r * j->in, wr, j->in);
+    }
+    return NULL;
+}
+
+/* cpu/mod.rs:199-229: element [r][o] = dot(x_row r, weight_row o). */
+void vo_oracle_matmul(const float *x, uint64_t rows, uint64_t in_features, const float *w,
+                      uint64_t out_features, float *out, int threads) {
+    if (threads < 1) threads = 1;
+    if ((uint64_t)threads > out_features) threads = out_features ? (int)out_features : 1;
+    matmul_job jobs[64];
+    pthread_t tid[64];
+    if (threads > 64) threads = 64;
+    uint64_t per = (out_features + (uint64_t)threads - 1) / (uint64_t)threads;
+    int started = 0;
+    for (int t = 0; t < threads; ++t) {
+        uint64_t b = (uint64_t)t * per, e = b + per;
+        if (e > out_features) e = out_features;
+        if (b >= e) break;
+        jobs[t] = (matmul_job){x, w, out, rows, in_features, out_features, b, e};
+        if (t == 0 || pthread_create(&tid[t], NULL, matmul_worker, &jobs[t]) != 0) {
+            if (t != 0) matmul_worker(&jobs[t]);
+            tid[t] = 0;
+        }
+        started = t + 1;
+    }
+    if (started > 0) matmul_worker(&jobs[0]);
+    for (int t = 1; t < started; ++t)
+        if (tid[t]) pthread_join(tid[t], NULL);
+}
+
+/* cpu/mod.rs:341-349: `*g = *g / (1.0 + (-*g).exp()) * u`. */
+void vo_oracle_silu_mul(float *gate, const float *up, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) gate[i] = gate[i] / (1.0f + expf(-gate[i])) * up[i];
+}
+
+/* cpu/mod.rs:351-358. */
+void vo_oracle_add(float *sum, const float *x, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) sum[i] += x[i];
+}
+
+/* cpu/mod.rs:360-368. */
+void vo_oracle_gather_rows(const float *x, uint64_t cols, const uint32_t *rows, uint64_t n,
+                           float *out) {
+    for (uint64_t i = 0; i < n; ++i)
+        memcpy(out + i * cols, x + (uint64_t)rows[i] * cols, cols * sizeof(float));
+}
+
+/* cpu/mod.rs:370-388.  The reference chunks rows*cols elements by
+ * `cols.max(1)`: with cols == 0 there are no elements and no rows. */
+int vo_oracle_argmax(const float *x, uint64_t rows, uint64_t cols, uint32_t *out) {
+    if (cols == 0) return VO_ORACLE_OK;
+    for (uint64_t r = 0; r < rows; ++r) {
+        const float *row = x + r * cols;
+        uint64_t best = 0;
+        for (uint64_t i = 0; i < cols; ++i) {
+            if (isnan(row[i])) return VO_ORACLE_NAN;
+            if (row[i] > row[best]) best = i;
+        }
+        out[r] = (uint32_t)best;
+    }
+    return VO_ORACLE_OK;
 }

@@ -19,7 +19,7 @@
  *
  * Status codes returned by the checking functions mirror EngineError
  * (error.rs:8-56): 0 = Ok, VO_ORACLE_BLOCK_TABLE_TOO_SHORT,
- * VO_ORACLE_SLOT_OUT_OF_RANGE, VO_ORACLE_BLOCK_OUT_OF_RANGE.
+ * VO_ORACLE_SLOT_OUT_OF_RANGE, VO_ORACLE_BLOCK_OUT_OF_RANGE, VO_ORACLE_NAN.
  */
 #ifndef VO_ORACLE_H
 #define VO_ORACLE_H
@@ -148,6 +148,41 @@ void vo_oracle_rope_table(const float *inv_freq, uint64_t half, uint64_t max_len
  * 2*half rotated at positions[r]. */
 void vo_oracle_rope_apply(float *x, uint64_t rows, uint64_t cols, const uint32_t *positions,
                           const float *cos_tab, const float *sin_tab, uint64_t half);
+
+/* ---- the rest of the layer: backend/cpu/mod.rs ---------------------- */
+
+enum { VO_ORACLE_NAN = 10 };
+
+/* cpu/mod.rs:172-180 (embed): out[r] = table[tokens[r]], table [vocab, hidden]. */
+void vo_oracle_embed(const float *table, uint64_t hidden, const uint32_t *tokens, uint64_t rows,
+                     float *out);
+
+/* cpu/mod.rs:182-197 (rmsnorm): mean_square = dot(x, x) / hidden (the 16-lane
+ * dot), inv_rms = 1 / sqrt(mean_square + eps), out = w * (x * inv_rms). */
+void vo_oracle_rmsnorm(const float *x, uint64_t rows, uint64_t hidden, const float *w, float eps,
+                       float *out);
+
+/* cpu/mod.rs:199-229 (matmul): out[r][o] = dot(x[r], w[o]) for x [rows, in],
+ * w [out_features, in].  Output columns are split over `threads` workers
+ * (rayon's weight-row chunks); each element is one dot, so the result does
+ * not depend on the thread count. */
+void vo_oracle_matmul(const float *x, uint64_t rows, uint64_t in_features, const float *w,
+                      uint64_t out_features, float *out, int threads);
+
+/* cpu/mod.rs:341-349 (silu_mul): gate[i] = gate[i] / (1 + exp(-gate[i])) * up[i]. */
+void vo_oracle_silu_mul(float *gate, const float *up, uint64_t n);
+
+/* cpu/mod.rs:351-358 (add): sum[i] += x[i]. */
+void vo_oracle_add(float *sum, const float *x, uint64_t n);
+
+/* cpu/mod.rs:360-368 (gather_rows): out[i] = x[rows[i]], rows of width cols. */
+void vo_oracle_gather_rows(const float *x, uint64_t cols, const uint32_t *rows, uint64_t n,
+                           float *out);
+
+/* cpu/mod.rs:370-388 (argmax): per row the first index of the maximum
+ * (strict '>' from index 0); VO_ORACLE_NAN when a NaN is met, scanning rows
+ * in order and each row from its start. */
+int vo_oracle_argmax(const float *x, uint64_t rows, uint64_t cols, uint32_t *out);
 
 #ifdef __cplusplus
 }

@@ -234,3 +234,83 @@ def cfg5_context_lens(seed=5, num_seqs=64, prefix=4096, lo=256, hi=1024, long_ct
     rng = np.random.default_rng(seed)
     ctx = prefix + rng.integers(lo, hi + 1, num_seqs)
     return np.concatenate([ctx, [long_ctx]])
+
+
+# ---- model configurations ----------------------------------------------------
+
+class ModelCfg:
+    """The ModelConfig fields (config.rs:9-34) with RopeScaling as a dict,
+    plus head_dim (config.rs:74-76).  Host-only, for the oracle and tests."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+        self.head_dim = self.hidden_size // self.num_attention_heads
+
+
+def tiny_config():
+    """testutil.rs:10-30: the reference's own test model."""
+    return ModelCfg(hidden_size=48, intermediate_size=80, num_hidden_layers=2,
+                    num_attention_heads=6, num_key_value_heads=2, vocab_size=37,
+                    max_position_embeddings=256, rms_norm_eps=1e-5, rope_theta=10000.0,
+                    rope_scaling=dict(factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                                      original_max_position_embeddings=64))
+
+
+def cfg1_config():
+    """the tiny Llama-style decoder (2 layers, hidden 256,
+    4 q / 2 kv heads, head_dim 64, FFN 688, vocab 1024, eps 1e-5, theta
+    10000).  Its rope_scaling block is the reference test model's
+    (testutil.rs:21-26): the reference's config always carries one."""
+    return ModelCfg(hidden_size=256, intermediate_size=688, num_hidden_layers=2,
+                    num_attention_heads=4, num_key_value_heads=2, vocab_size=1024,
+                    max_position_embeddings=256, rms_norm_eps=1e-5, rope_theta=10000.0,
+                    rope_scaling=dict(factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                                      original_max_position_embeddings=64))
+
+
+def llama3_8b_config(num_hidden_layers=32):
+    """Llama-3-8B shape (32 layers, hidden 4096, 32 q / 8 kv
+    heads, head_dim 128, FFN 14336, vocab 128256, theta 500000).  Llama 3 8B
+    has no rope_scaling; factor 1 with the 1-4 bands leaves every frequency
+    at its raw value up to the blend's rounding."""
+    return ModelCfg(hidden_size=4096, intermediate_size=14336,
+                    num_hidden_layers=num_hidden_layers, num_attention_heads=32,
+                    num_key_value_heads=8, vocab_size=128256, max_position_embeddings=8192,
+                    rms_norm_eps=1e-5, rope_theta=500000.0,
+                    rope_scaling=dict(factor=1.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                                      original_max_position_embeddings=8192))
+
+
+def normal_weights(cfg, seed, std=0.02):
+    """BASELINE configs 1 and 4: weights ~ N(0, std) (f32 numpy, seeded),
+    norm weights 1."""
+    rng = np.random.default_rng(seed)
+    h, hd = cfg.hidden_size, cfg.head_dim
+    qd, kvd, f = cfg.num_attention_heads * hd, cfg.num_key_value_heads * hd, cfg.intermediate_size
+
+    def m(o, i):
+        return (rng.standard_normal((o, i), np.float32) * np.float32(std)).astype(np.float32)
+
+    layers = [dict(attn_norm=np.ones(h, np.float32), wq=m(qd, h), wk=m(kvd, h), wv=m(kvd, h),
+                   wo=m(h, qd), mlp_norm=np.ones(h, np.float32), w_gate=m(f, h), w_up=m(f, h),
+                   w_down=m(h, f)) for _ in range(cfg.num_hidden_layers)]
+    return dict(embed=m(cfg.vocab_size, h), layers=layers, final_norm=np.ones(h, np.float32))
+
+
+def round_bf16(a):
+    """f32 -> nearest bf16 (ties to even) -> f32, on the host."""
+    a = np.ascontiguousarray(a, np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def bf16_weights(w):
+    """The same weights rounded to bf16 (what the GPU model holds), as f32."""
+    return dict(embed=round_bf16(w["embed"]), final_norm=round_bf16(w["final_norm"]),
+                layers=[{k: round_bf16(v) for k, v in L.items()} for L in w["layers"]])
+
+
+def ref_prompt(n, seed):
+    """model.rs:385-389: the reference's test prompts over a 37-token vocab."""
+    return [(i * 7 + seed * 13 + 3) % 37 for i in range(n)]

@@ -22,6 +22,7 @@ from __future__ import annotations
 import ctypes
 import os
 import pathlib
+import weakref
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
 
@@ -50,6 +51,9 @@ VO_ERR_DEVICE = 6
 VO_ERR_INVALID_ARGUMENT = 7
 VO_ERR_UNSUPPORTED = 8
 VO_ERR_POSITION_OUT_OF_RANGE = 9
+VO_ERR_NAN = 10
+VO_DTYPE_BF16 = 0
+VO_DTYPE_F32 = 1
 
 _u64 = ctypes.c_uint64
 _u32p = ctypes.POINTER(ctypes.c_uint32)
@@ -145,6 +149,20 @@ SIGNATURES = {
     "vo_rope": (ctypes.c_int32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp]),
     "vo_rope_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _vp, _vp, _u64, _u64, _vp,
                                           _vp]),
+    "vo_qkv_rope_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _u64, _vp, _vp,
+                                              _vp]),
+    "vo_step_meta_upload_tokens": (ctypes.c_int32, [_vp, _u32p, _u64, _vp]),
+    "vo_embed": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp]),
+    "vo_rmsnorm": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp, _vp]),
+    "vo_rmsnorm_last_rows": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp,
+                                              _vp, _vp]),
+    "vo_add": (ctypes.c_int32, [_vp, _vp, ctypes.c_int32, _u64, _u64, _vp]),
+    "vo_silu_mul": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _u64, _vp, _u64, _vp]),
+    "vo_argmax": (ctypes.c_int32, [_vp, ctypes.c_int32, _u64, _u64, _u32p, _u32p, _vp]),
+    "vo_gemm_create": (ctypes.c_int32, [ctypes.c_int32, _u64, ctypes.POINTER(_vp)]),
+    "vo_gemm_destroy": (None, [_vp]),
+    "vo_matmul": (ctypes.c_int32, [_vp, _vp, _u64, _u64, _vp, _u64, _u64, _vp, ctypes.c_int32,
+                                   ctypes.c_int32, _vp]),
     "vo_profiling_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "vo_profile_read": (ctypes.c_int32, [ctypes.POINTER(vo_kernel_stat), _u64, _u64p]),
     "vo_profile_reset": (None, []),
@@ -218,6 +236,7 @@ class DeviceError(EngineError): pass
 class InvalidArgument(EngineError): pass
 class Unsupported(EngineError): pass
 class PositionOutOfRange(EngineError): pass
+class NaNError(EngineError): pass
 
 
 _ERROR_CLASSES = {
@@ -225,8 +244,19 @@ _ERROR_CLASSES = {
     VO_ERR_BLOCK_TABLE_TOO_SHORT: BlockTableTooShort, VO_ERR_SLOT_OUT_OF_RANGE: SlotOutOfRange,
     VO_ERR_BLOCK_OUT_OF_RANGE: BlockOutOfRange, VO_ERR_DEVICE: DeviceError,
     VO_ERR_INVALID_ARGUMENT: InvalidArgument, VO_ERR_UNSUPPORTED: Unsupported,
-    VO_ERR_POSITION_OUT_OF_RANGE: PositionOutOfRange,
+    VO_ERR_POSITION_OUT_OF_RANGE: PositionOutOfRange, VO_ERR_NAN: NaNError,
 }
+
+
+def _engine_error(cls, status: int, op: str, message: str, value: int = 0, limit: int = 0):
+    """An EngineError raised by host code above the C ABI (the model's batch
+    checks, model.rs:245-267), with the same fields as one from the library."""
+    info = vo_error_info()
+    info.status = status
+    info.op = op.encode()[:47]
+    info.value, info.limit = value, limit
+    info.message = message.encode()[:255]
+    return cls(info)
 
 
 def _check(rc: int) -> None:
@@ -485,6 +515,12 @@ class StepMeta:
             raise TypeError(f"cannot upload {type(meta).__name__}")
         self.holds = meta
 
+    def upload_tokens(self, tokens, stream=None) -> None:
+        """The step's token ids (vo_step_meta_upload_tokens)."""
+        t = _u32(tokens) if len(tokens) else np.zeros(1, np.uint32)
+        _check(lib.vo_step_meta_upload_tokens(self._h, _p32(t), len(tokens),
+                                              _stream_ptr(stream)))
+
     def upload_slots(self, slots, stream=None) -> None:
         s = _u32(slots)
         _check(lib.vo_step_meta_upload_slots(self._h, _p32(s), len(s), _stream_ptr(stream)))
@@ -517,6 +553,16 @@ def _dev_ptr(t) -> _vp:
         raise TypeError("expected a device tensor")
     if t.dtype != torch.bfloat16 or not t.is_contiguous():
         raise TypeError("expected a contiguous bfloat16 tensor")
+    return _vp(t.data_ptr())
+
+
+def _any_ptr(t, dtype) -> _vp:
+    """Device pointer of a contiguous tensor of the given torch dtype."""
+    import torch
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError("expected a device tensor")
+    if t.dtype != dtype or not t.is_contiguous():
+        raise TypeError(f"expected a contiguous {dtype} tensor, got {t.dtype}")
     return _vp(t.data_ptr())
 
 
@@ -633,7 +679,9 @@ class HipBackend:
                  max_table_entries: int = 1 << 16, max_query_heads: int = 64):
         self.device = device
         self._caps = (max_seqs, max_rows, max_table_entries, max_query_heads)
-        self._metas = {}
+        # pool -> {slot name: StepMeta}; keyed by the pool object itself (weakly),
+        # so a meta never outlives its pool or serves a later pool.
+        self._metas = weakref.WeakKeyDictionary()
 
     def name(self) -> str:
         return "hip-gfx950"
@@ -649,11 +697,11 @@ class HipBackend:
                         out.head_dim)
 
     def step_meta(self, pool: KvPool, slot: str = "step") -> StepMeta:
-        key = (id(pool), slot)
-        m = self._metas.get(key)
+        per_pool = self._metas.setdefault(pool, {})
+        m = per_pool.get(slot)
         if m is None:
             m = StepMeta(pool, *self._caps)
-            self._metas[key] = m
+            per_pool[slot] = m
         return m
 
     def _meta_for(self, pool: KvPool, meta, stream) -> StepMeta:
@@ -722,6 +770,82 @@ class HipBackend:
                          stream=None):
         return self._attention(lib.vo_decode_attention, queries, pool, layer, meta, out, stream)
 
+    # ---- the rest of the layer (model.rs:269-356) ------------------------
+    def embed(self, table, tokens, meta_holder: StepMeta, stream=None):
+        """Backend::embed: [T, hidden] f32 rows of the bf16 table."""
+        import torch
+        meta_holder.upload_tokens(tokens, stream)
+        out = torch.empty((len(tokens), table.shape[1]), dtype=torch.float32,
+                          device=f"cuda:{self.device}")
+        _check(lib.vo_embed(_dev_ptr(table), table.shape[0], table.shape[1], meta_holder.handle,
+                            len(tokens), _any_ptr(out, torch.float32), _stream_ptr(stream)))
+        return out
+
+    def rmsnorm(self, x, weight, eps: float, stream=None):
+        """Backend::rmsnorm: x [T, H] f32, weight [H] bf16 -> [T, H] bf16."""
+        import torch
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+        _check(lib.vo_rmsnorm(_any_ptr(x, torch.float32), x.shape[0], x.shape[1],
+                              _dev_ptr(weight), weight.numel(), eps, _dev_ptr(out),
+                              _stream_ptr(stream)))
+        return out
+
+    def rmsnorm_last_rows(self, x, weight, eps: float, pool: KvPool, meta, stream=None):
+        """gather_rows(x, meta.last_rows()) then rmsnorm, one pass -> [S, H] bf16."""
+        import torch
+        m = self._meta_for(pool, meta, stream)
+        out = torch.empty((meta.num_seqs(), x.shape[1]), dtype=torch.bfloat16, device=x.device)
+        _check(lib.vo_rmsnorm_last_rows(_any_ptr(x, torch.float32), x.shape[0], x.shape[1],
+                                        _dev_ptr(weight), weight.numel(), eps, m.handle,
+                                        _dev_ptr(out), _stream_ptr(stream)))
+        return out
+
+    def add(self, total, x, stream=None) -> None:
+        """Backend::add: total (f32) += x (bf16 or f32), in place."""
+        import torch
+        if tuple(total.shape) != tuple(x.shape):
+            raise ValueError("add: shapes differ")
+        dt = VO_DTYPE_BF16 if x.dtype == torch.bfloat16 else VO_DTYPE_F32
+        _check(lib.vo_add(_any_ptr(total, torch.float32), _any_ptr(x, x.dtype), dt,
+                          total.shape[0], total.shape[1], _stream_ptr(stream)))
+
+    def silu_mul(self, gate, up, out=None, stream=None):
+        """Backend::silu_mul: out = silu(gate) * up (out=gate: in place); 2-D
+        bf16 tensors whose rows may be strided."""
+        import torch
+        if out is None:
+            out = torch.empty(gate.shape, dtype=torch.bfloat16, device=gate.device)
+        for t in (gate, up, out):
+            if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+                raise TypeError("silu_mul takes 2-D bfloat16 tensors with unit column stride")
+        _check(lib.vo_silu_mul(_vp(gate.data_ptr()), gate.stride(0), _vp(up.data_ptr()),
+                               up.stride(0), gate.shape[0], gate.shape[1], _vp(out.data_ptr()),
+                               out.stride(0), _stream_ptr(stream)))
+        return out
+
+    def argmax(self, logits, stream=None) -> np.ndarray:
+        """Backend::argmax: first index of each row's maximum; NaNError on a NaN."""
+        import torch
+        rows = logits.shape[0]
+        ids = torch.empty((max(rows, 1),), dtype=torch.int32, device=logits.device)
+        host = np.zeros(max(rows, 1), np.uint32)
+        dt = VO_DTYPE_F32 if logits.dtype == torch.float32 else VO_DTYPE_BF16
+        _check(lib.vo_argmax(_any_ptr(logits, logits.dtype), dt, rows, logits.shape[1],
+                             ctypes.cast(ctypes.c_void_p(ids.data_ptr()), _u32p), _p32(host),
+                             _stream_ptr(stream)))
+        return host[:rows]
+
+    def gemm(self) -> "Gemm":
+        g = getattr(self, "_gemm", None)
+        if g is None:
+            g = self._gemm = Gemm(self.device)
+        return g
+
+    def matmul(self, x, weight, out_dtype=None, out=None, accumulate=False, stream=None):
+        """Backend::matmul: x [T, in] bf16 . weight [out, in]^T (bf16) on hipBLASLt;
+        accumulate: out += (out f32 or bf16)."""
+        return self.gemm().matmul(x, weight, out_dtype, out, accumulate, stream)
+
     def read_kv(self, pool: KvPool, layer: int, meta, seq: int, num_keys: int, stream=None):
         """Keys and values 0..num_keys of sequence ``seq``, [num_keys, kv_heads*head_dim]."""
         import torch
@@ -733,6 +857,43 @@ class HipBackend:
         _check(lib.vo_gather_kv(pool.handle, layer, m.handle, seq, num_keys, _dev_ptr(k),
                                 _dev_ptr(v), _stream_ptr(stream)))
         return k[:num_keys], v[:num_keys]
+
+
+class Gemm:
+    """vo_gemm: hipBLASLt handle, workspace and per-shape plans on one device."""
+
+    def __init__(self, device: int = 0, workspace_bytes: int = 128 << 20):
+        self._h = _vp()
+        _check(lib.vo_gemm_create(device, workspace_bytes, ctypes.byref(self._h)))
+
+    @property
+    def handle(self):
+        return self._h
+
+    def matmul(self, x, weight, out_dtype=None, out=None, accumulate=False, stream=None):
+        import torch
+        if out_dtype is None:
+            out_dtype = out.dtype if out is not None else torch.bfloat16
+        if out is None:
+            if accumulate:
+                raise ValueError("accumulate needs an output to add into")
+            out = torch.empty((x.shape[0], weight.shape[0]), dtype=out_dtype, device=x.device)
+        dt = VO_DTYPE_F32 if out_dtype == torch.float32 else VO_DTYPE_BF16
+        _check(lib.vo_matmul(self._h, _dev_ptr(x), x.shape[0], x.shape[1], _dev_ptr(weight),
+                             weight.shape[0], weight.shape[1], _any_ptr(out, out_dtype), dt,
+                             int(bool(accumulate)), _stream_ptr(stream)))
+        return out
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_gemm_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def prefill_meta_build_device(seq_row_starts, context_lens, table_off, tables, block_size: int,

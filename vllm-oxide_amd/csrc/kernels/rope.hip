@@ -20,7 +20,9 @@
 // wavefront rotates the run's q rows for the G query heads of its KV head in
 // place, writes the rotated K into the key-major tile and V into the
 // dim-major tile (transposed in registers, 32-byte runs per dim for a whole
-// block), reading each row's cos/sin once.
+// block), reading each row's cos/sin once.  q may be read from one buffer
+// and written to another (the rows of a fused QKV projection output are
+// strided: q_in_ld, kv_ld), or rotated in place (q_in == q_out).
 //
 // Roofline: HBM.  Bytes per row = q read + written, k and v read and written
 // to the pool, cos/sin 2*half*4*2 (mostly cache hits).
@@ -108,8 +110,9 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(uint16_t *__restrict__ x
 template <int HD>
 __global__ __launch_bounds__(256) void rope_cache_kernel(
     uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool, uint32_t kv_heads,
-    uint16_t *__restrict__ q, uint32_t q_cols, uint32_t group, const uint16_t *__restrict__ keys,
-    const uint16_t *__restrict__ values, const uint32_t *__restrict__ segments,
+    const uint16_t *q_in, uint32_t q_in_ld, uint16_t *q_out, uint32_t q_out_ld, uint32_t group,
+    const uint16_t *__restrict__ keys, const uint16_t *__restrict__ values, uint32_t kv_ld,
+    const uint32_t *__restrict__ segments,
     const uint32_t *__restrict__ positions, const float *__restrict__ cos_tab,
     const float *__restrict__ sin_tab, uint32_t num_items) {
     constexpr uint32_t BS = 16;
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
     // A superseded row (slot kSkipSlot) only has its q rotated.
     const bool cache = slot0 != kSkipSlot;
     const uint32_t off0 = cache ? slot0 % BS : 0;
-    const uint64_t width = static_cast<uint64_t>(kv_heads) * HD;
+    const uint64_t width = kv_ld;
     const uint64_t tile = cache ? (static_cast<uint64_t>(slot0 / BS) * kv_heads + kvh) * (BS * HD) : 0;
 
     const uint32_t u = lane % UPR;
@@ -168,10 +171,11 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
         if (live && cache)
             *reinterpret_cast<u32x4 *>(k_pool + tile + (d / 32) * (BS * 32) + (off0 + i) * 32 + d % 32) = kout;
         for (uint32_t h = 0; h < group; ++h) {
-            uint16_t *qp = q + static_cast<uint64_t>(row) * q_cols + (kvh * group + h) * HD + d;
-            const u32x4 qin = *reinterpret_cast<const u32x4 *>(qp);
+            const uint32_t col = (kvh * group + h) * HD + d;
+            const u32x4 qin =
+                *reinterpret_cast<const u32x4 *>(q_in + static_cast<uint64_t>(row) * q_in_ld + col);
             const u32x4 qout = rot(qin, c, s);
-            if (live) *reinterpret_cast<u32x4 *>(qp) = qout;
+            if (live) *reinterpret_cast<u32x4 *>(q_out + static_cast<uint64_t>(row) * q_out_ld + col) = qout;
         }
     }
 
@@ -236,10 +240,11 @@ hipError_t launch_rope_rows(uint16_t *x, uint32_t rows, uint32_t cols, uint32_t 
     return hipGetLastError();
 }
 
-hipError_t launch_rope_cache(const PoolLayer &pool, uint16_t *q, uint32_t q_cols, uint32_t group,
-                             const uint16_t *keys, const uint16_t *values, const WritePlan &plan,
-                             const uint32_t *positions, const float *cos_tab, const float *sin_tab,
-                             hipStream_t stream) {
+hipError_t launch_rope_cache(const PoolLayer &pool, const uint16_t *q_in, uint32_t q_in_ld,
+                             uint16_t *q_out, uint32_t q_out_ld, uint32_t group,
+                             const uint16_t *keys, const uint16_t *values, uint32_t kv_ld,
+                             const WritePlan &plan, const uint32_t *positions,
+                             const float *cos_tab, const float *sin_tab, hipStream_t stream) {
     if (plan.num_segments == 0) return hipSuccess;
     if (!cache_write_supported(pool.head_dim, pool.block_size)) return hipErrorInvalidValue;
     const uint64_t items = static_cast<uint64_t>(plan.num_segments) * pool.kv_heads;
@@ -248,13 +253,13 @@ hipError_t launch_rope_cache(const PoolLayer &pool, uint16_t *q, uint32_t q_cols
     KernelTimer timer("rope_cache", stream);
     if (pool.head_dim == 128)
         hipLaunchKernelGGL((rope_cache_kernel<128>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
-                           stream, pool.k, pool.v, pool.kv_heads, q, q_cols, group, keys, values,
-                           plan.segments, positions, cos_tab, sin_tab,
+                           stream, pool.k, pool.v, pool.kv_heads, q_in, q_in_ld, q_out, q_out_ld, group,
+                           keys, values, kv_ld, plan.segments, positions, cos_tab, sin_tab,
                            static_cast<uint32_t>(items));
     else
         hipLaunchKernelGGL((rope_cache_kernel<64>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
-                           stream, pool.k, pool.v, pool.kv_heads, q, q_cols, group, keys, values,
-                           plan.segments, positions, cos_tab, sin_tab,
+                           stream, pool.k, pool.v, pool.kv_heads, q_in, q_in_ld, q_out, q_out_ld, group,
+                           keys, values, kv_ld, plan.segments, positions, cos_tab, sin_tab,
                            static_cast<uint32_t>(items));
     return hipGetLastError();
 }

@@ -70,11 +70,14 @@ hipError_t launch_rope_rows(uint16_t *x, uint32_t rows, uint32_t cols, uint32_t 
                             const uint32_t *positions, const float *cos_tab, const float *sin_tab,
                             hipStream_t stream);
 
-// rope(q) in place + rope(k) and v into the pool over the write plan.
-hipError_t launch_rope_cache(const PoolLayer &pool, uint16_t *q, uint32_t q_cols, uint32_t group,
-                             const uint16_t *keys, const uint16_t *values, const WritePlan &plan,
-                             const uint32_t *positions, const float *cos_tab, const float *sin_tab,
-                             hipStream_t stream);
+// rope(q) (q_in -> q_out, which may be the same rows) + rope(k) and v into
+// the pool over the write plan.  Row strides in elements: q_in_ld, q_out_ld,
+// kv_ld (keys and values).
+hipError_t launch_rope_cache(const PoolLayer &pool, const uint16_t *q_in, uint32_t q_in_ld,
+                             uint16_t *q_out, uint32_t q_out_ld, uint32_t group,
+                             const uint16_t *keys, const uint16_t *values, uint32_t kv_ld,
+                             const WritePlan &plan, const uint32_t *positions,
+                             const float *cos_tab, const float *sin_tab, hipStream_t stream);
 
 // reshape_and_cache: pool[slot_mapping[t]] = keys[t], values[t].
 // keys/values: [rows, kv_heads*head_dim] bf16.  Rows whose slot is
@@ -117,6 +120,23 @@ hipError_t launch_build_rows(const uint32_t *seq_row_starts, const uint32_t *con
                              uint32_t num_rows, uint32_t block_size, uint32_t *positions,
                              uint32_t *slot_mapping, uint32_t *row_seq, uint32_t *row_num_keys,
                              uint32_t *errors, hipStream_t stream);
+
+// The layer's ops around attention (layer_ops.hip).  rows_idx (device, may
+// be null) selects the rows of x that rmsnorm normalises.
+hipError_t launch_embed(const uint16_t *table, uint32_t hidden, const uint32_t *tokens,
+                        uint32_t rows, float *out, hipStream_t stream);
+hipError_t launch_rmsnorm(const float *x, uint32_t hidden, const uint16_t *weight, float eps,
+                          const uint32_t *rows_idx, uint32_t rows, uint16_t *out,
+                          hipStream_t stream);
+hipError_t launch_add(float *sum, const void *x, bool x_bf16, uint64_t n, hipStream_t stream);
+hipError_t launch_silu_mul(const uint16_t *gate, uint32_t gate_ld, const uint16_t *up,
+                           uint32_t up_ld, uint32_t rows, uint32_t cols, uint16_t *out,
+                           uint32_t out_ld, bool vec8, hipStream_t stream);
+hipError_t launch_argmax(const void *logits, bool f32, uint32_t rows, uint32_t cols, uint32_t *ids,
+                         hipStream_t stream);
+hipError_t launch_matmul_generic(const uint16_t *x, const uint16_t *w, uint32_t rows, uint32_t n,
+                                 uint32_t k, void *out, bool out_f32, bool accumulate,
+                                 hipStream_t stream);
 
 // Largest split the decode kernel takes (its block-table slice lives in LDS).
 constexpr uint32_t kMaxSplitKeys = 4096;

@@ -16,65 +16,13 @@
 #include <unordered_map>
 #include <vector>
 
-#include "kernels/vo_kernels.hpp"
-#include "vo_paged.hpp"
+#include "vo_backend.hpp"
 
 using namespace vo;
-
-namespace {
-
-constexpr uint32_t kSkipSlot = 0xffffffffu;  // row superseded by a later row
-constexpr uint64_t kU32Limit = 0x7fffffffull;
-
-// Makes `device` current for the scope and restores the caller's device.
-class DeviceGuard {
-   public:
-    explicit DeviceGuard(int device) {
-        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
-        if (prev_ != device) ok_ = hipSetDevice(device) == hipSuccess;
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
-    }
-    bool ok() const { return ok_; }
-
-   private:
-    int prev_ = -1;
-    bool ok_ = true;
-};
-
-uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
-
-int env_int(const char *name, int fallback) {
-    const char *v = std::getenv(name);
-    if (!v || !*v) return fallback;
-    return std::atoi(v);
-}
-
-}  // namespace
 
 // ---------------------------------------------------------------------------
 // KV pool
 // ---------------------------------------------------------------------------
-struct vo_kv_pool {
-    vo_kv_layout layout{};
-    int device = 0;
-    int num_cus = 256;
-    uint16_t *base = nullptr;   // [layers][K|V][layer_elems] bf16
-    uint64_t layer_elems = 0;   // elements of one layer's K (or V)
-    uint64_t bytes = 0;
-
-    kernels::PoolLayer layer(uint64_t l) const {
-        kernels::PoolLayer p;
-        p.k = base + l * 2 * layer_elems;
-        p.v = p.k + layer_elems;
-        p.kv_heads = static_cast<uint32_t>(layout.kv_heads);
-        p.head_dim = static_cast<uint32_t>(layout.head_dim);
-        p.block_size = static_cast<uint32_t>(layout.block_size);
-        return p;
-    }
-};
 
 extern "C" int32_t vo_kv_pool_create(const vo_kv_layout *layout, int32_t device,
                                      vo_kv_pool **out) {
@@ -138,64 +86,6 @@ extern "C" uint64_t vo_kv_pool_bytes(const vo_kv_pool *pool) { return pool ? poo
 // ---------------------------------------------------------------------------
 // Step metadata
 // ---------------------------------------------------------------------------
-namespace {
-enum MetaKind { kNone = 0, kPrefill = 1, kDecode = 2, kSlots = 3 };
-}
-
-// A row's last, shorter split in the decode work order (keys < split size).
-struct TailItem {
-    uint32_t keys, row, split;
-};
-
-struct vo_step_meta {
-    int device = 0;
-    int num_cus = 256;
-    uint64_t pool_block_size = 0;
-    uint64_t kv_heads = 0;
-    uint64_t head_dim = 0;
-
-    uint64_t max_seqs = 0, max_rows = 0, max_entries = 0, max_heads = 0, max_parts = 0;
-
-    MetaKind kind = kNone;
-    uint64_t block_size = 0;
-    uint64_t num_seqs = 0;
-    uint64_t num_rows = 0;
-
-    // Host copies, for validation with the reference's error semantics.
-    std::vector<uint64_t> table_off;    // [S+1]
-    std::vector<uint32_t> tables;       // [entries]
-    std::vector<uint32_t> slots;        // [T] as given
-    std::vector<uint32_t> row_seq;      // [T]
-    std::vector<uint32_t> row_num_keys; // [T]
-    uint32_t max_block = 0;             // max table entry (0 if none)
-    uint32_t max_slot = 0;              // max slot (0 if none)
-    bool has_positions = false;         // positions were uploaded (RoPE needs them)
-    std::vector<uint32_t> positions;    // [T] when uploaded
-    uint32_t max_position = 0;          // largest position (0 if none)
-
-    // Device buffer and pinned staging of the same size.
-    uint8_t *d_buf = nullptr;
-    uint8_t *h_stage = nullptr;
-    uint64_t buf_bytes = 0;
-    hipEvent_t copy_done = nullptr;
-    bool copy_pending = false;
-
-    // Split-K partials (fp32).
-    float *d_part_acc = nullptr;
-    float *d_part_ml = nullptr;
-
-    kernels::MetaView view{};
-    const uint32_t *d_write_slots = nullptr;  // slots with superseded rows = kSkipSlot
-    kernels::WritePlan write_plan{};          // runs of consecutive slots inside one block
-    kernels::DecodePlan plan{};
-    bool decode_planned = false;
-    std::vector<TailItem> tail_items;  // scratch of plan_decode (capacity kept across steps)
-    std::vector<uint8_t> block_seen;   // scratch of plan_decode: one byte per physical block
-    std::vector<uint64_t> seq_keys;    // scratch of plan_decode: keys read per sequence
-    std::vector<uint32_t> decode_rows; // rows of a prefill step planned on the decode kernel
-    kernels::PrefillPlan prefill_plan{};
-    bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
-};
 
 namespace {
 
@@ -398,6 +288,8 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     m->view.num_rows = static_cast<uint32_t>(num_rows);
     m->view.num_seqs = static_cast<uint32_t>(num_seqs);
     m->decode_planned = false;
+    m->d_last_rows = nullptr;
+    m->last_rows_ok = false;
     return VO_OK;
 }
 
@@ -617,7 +509,8 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
                           + max_rows                                         // positions
                           + 2 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
-                          + 8 * 64;                                          // alignment slack
+                          + max_seqs                                         // last rows
+                          + 9 * 64;                                          // alignment slack
     m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
     hipError_t err = hipMalloc(reinterpret_cast<void **>(&m->d_buf), m->buf_bytes);
     if (err == hipSuccess)
@@ -629,8 +522,17 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
         err = hipMalloc(reinterpret_cast<void **>(&m->d_part_ml),
                         m->max_parts * max_query_heads * 2 * sizeof(float));
     if (err == hipSuccess) err = hipEventCreateWithFlags(&m->copy_done, hipEventDisableTiming);
+    if (err == hipSuccess)
+        err = hipMalloc(reinterpret_cast<void **>(&m->d_tokens), max_rows * sizeof(uint32_t));
+    if (err == hipSuccess)
+        err = hipHostMalloc(reinterpret_cast<void **>(&m->h_tokens), max_rows * sizeof(uint32_t),
+                            hipHostMallocDefault);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&m->tokens_done, hipEventDisableTiming);
     if (err != hipSuccess) {
         vo_status rc = fail_device(op, err, hipGetErrorString(err));
+        if (m->d_tokens) (void)hipFree(m->d_tokens);
+        if (m->h_tokens) (void)hipHostFree(m->h_tokens);
+        if (m->tokens_done) (void)hipEventDestroy(m->tokens_done);
         if (m->d_buf) (void)hipFree(m->d_buf);
         if (m->h_stage) (void)hipHostFree(m->h_stage);
         if (m->d_part_acc) (void)hipFree(m->d_part_acc);
@@ -649,6 +551,10 @@ extern "C" void vo_step_meta_destroy(vo_step_meta *m) {
     DeviceGuard guard(m->device);
     if (m->copy_pending) (void)hipEventSynchronize(m->copy_done);
     if (m->copy_done) (void)hipEventDestroy(m->copy_done);
+    if (m->tokens_pending) (void)hipEventSynchronize(m->tokens_done);
+    if (m->tokens_done) (void)hipEventDestroy(m->tokens_done);
+    (void)hipFree(m->d_tokens);
+    (void)hipHostFree(m->h_tokens);
     (void)hipFree(m->d_buf);
     (void)hipHostFree(m->h_stage);
     (void)hipFree(m->d_part_acc);
@@ -679,6 +585,17 @@ extern "C" int32_t vo_step_meta_upload_prefill(
         m->kind = kNone;
         return rc;
     }
+    {
+        // PrefillMeta::last_rows (paged.rs:153-159).
+        const uint32_t *dp;
+        uint32_t *h = pk.add(num_seqs, &dp);
+        m->last_rows_ok = true;
+        for (uint64_t s = 0; s < num_seqs; ++s) {
+            if (seq_row_starts[s + 1] == seq_row_starts[s]) m->last_rows_ok = false;
+            h[s] = seq_row_starts[s + 1] ? static_cast<uint32_t>(seq_row_starts[s + 1] - 1) : 0u;
+        }
+        m->d_last_rows = dp;
+    }
     if (!pk.fits()) {
         m->kind = kNone;
         return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
@@ -704,6 +621,14 @@ extern "C" int32_t vo_step_meta_upload_decode(vo_step_meta *m, uint64_t block_si
     if (vo_status rc = plan_decode(m, pk)) {
         m->kind = kNone;
         return rc;
+    }
+    {
+        // Decode: every row is its sequence's last (model.rs:342).
+        const uint32_t *dp;
+        uint32_t *h = pk.add(num_seqs, &dp);
+        for (uint64_t s = 0; s < num_seqs; ++s) h[s] = static_cast<uint32_t>(s);
+        m->d_last_rows = dp;
+        m->last_rows_ok = true;
     }
     if (!pk.fits()) {
         m->kind = kNone;
@@ -737,13 +662,6 @@ extern "C" int32_t vo_step_meta_upload_slots(vo_step_meta *m, const uint32_t *sl
 // Ops
 // ---------------------------------------------------------------------------
 namespace {
-
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-bool overlaps(const void *a, uint64_t a_bytes, const void *b, uint64_t b_bytes) {
-    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
-    return a_bytes && b_bytes && a0 < b0 + b_bytes && b0 < a0 + a_bytes;
-}
 
 std::string layout_text(const vo_kv_layout &L) {
     return "KvLayout { num_layers: " + std::to_string(L.num_layers) +
@@ -788,11 +706,6 @@ vo_status check_attention(const char *op, const void *queries, uint64_t rows, ui
     return VO_OK;
 }
 
-vo_status device_status(const char *op, hipError_t err) {
-    if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
-    clear_error();
-    return VO_OK;
-}
 
 }  // namespace
 
@@ -871,12 +784,6 @@ extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *key
 // ---------------------------------------------------------------------------
 // RoPE
 // ---------------------------------------------------------------------------
-struct vo_rope_table {
-    int device = 0;
-    uint64_t head_dim = 0, half = 0, max_len = 0;
-    float *d_cos = nullptr;  // [max_len][half]
-    float *d_sin = nullptr;
-};
 
 namespace {
 
@@ -1050,9 +957,48 @@ extern "C" int32_t vo_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_r
     DeviceGuard guard(pool->device);
     const uint32_t group = static_cast<uint32_t>(q_cols / L.head_dim / L.kv_heads);
     const hipError_t err = kernels::launch_rope_cache(
-        pool->layer(layer), static_cast<uint16_t *>(queries), static_cast<uint32_t>(q_cols), group,
-        static_cast<const uint16_t *>(keys), static_cast<const uint16_t *>(values), m->write_plan,
-        m->view.positions, t->d_cos, t->d_sin, static_cast<hipStream_t>(stream));
+        pool->layer(layer), static_cast<const uint16_t *>(queries), static_cast<uint32_t>(q_cols),
+        static_cast<uint16_t *>(queries), static_cast<uint32_t>(q_cols), group,
+        static_cast<const uint16_t *>(keys), static_cast<const uint16_t *>(values),
+        static_cast<uint32_t>(kv_cols), m->write_plan, m->view.positions, t->d_cos, t->d_sin,
+        static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_qkv_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_rope_table *t,
+                                        const void *qkv, uint64_t rows, uint64_t q_cols,
+                                        uint64_t kv_cols, const vo_step_meta *m, void *q_out,
+                                        void *stream) {
+    const char *op = "rope_write_kv";
+    if (!pool || !t || !m) return fail_argument(op, "null pool, table or meta");
+    const vo_kv_layout &L = pool->layout;
+    if (vo_status rc = check_rope("rope", t, rows, q_cols, L.head_dim, m)) return rc;
+    if (vo_status rc = check_rope("rope", t, rows, kv_cols, L.head_dim, m)) return rc;
+    if (!kernels::cache_write_supported(static_cast<uint32_t>(L.head_dim),
+                                        static_cast<uint32_t>(L.block_size)))
+        return fail_unsupported(op, "the fused write needs block size 16 and head_dim 64 or 128");
+    if (vo_status rc = check_write(pool, layer, rows, kv_cols, m)) return rc;
+    if (q_cols % (L.kv_heads * L.head_dim) != 0)
+        return fail_shape(op, "q_cols " + std::to_string(q_cols) + " is not a multiple of kv_heads * head_dim");
+    const uint64_t ld = q_cols + 2 * kv_cols;
+    if (ld > kU32Limit) return fail_capacity("qkv columns (u32)", ld, kU32Limit);
+    if (rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!qkv || !q_out) return fail_argument(op, "null qkv or q_out");
+    if (!aligned16(qkv) || !aligned16(q_out))
+        return fail_argument(op, "qkv and q_out must be 16-byte aligned");
+    if (overlaps(qkv, rows * ld * 2, q_out, rows * q_cols * 2))
+        return fail_shape(op, "q_out overlaps qkv");
+    DeviceGuard guard(pool->device);
+    const uint32_t group = static_cast<uint32_t>(q_cols / L.head_dim / L.kv_heads);
+    const uint16_t *base = static_cast<const uint16_t *>(qkv);
+    const hipError_t err = kernels::launch_rope_cache(
+        pool->layer(layer), base, static_cast<uint32_t>(ld), static_cast<uint16_t *>(q_out),
+        static_cast<uint32_t>(q_cols), group, base + q_cols, base + q_cols + kv_cols,
+        static_cast<uint32_t>(ld), m->write_plan, m->view.positions, t->d_cos, t->d_sin,
+        static_cast<hipStream_t>(stream));
     return device_status(op, err);
 }
 

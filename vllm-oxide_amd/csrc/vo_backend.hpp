@@ -1,0 +1,157 @@
+// vo_backend.hpp -- private to the library: the opaque C types behind the
+// ABI (KV pool, step metadata, RoPE table) and the helpers the op files share.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+#include "kernels/vo_kernels.hpp"
+#include "vo_paged.hpp"
+
+namespace vo {
+
+constexpr uint32_t kSkipSlot = 0xffffffffu;  // row superseded by a later row
+constexpr uint64_t kU32Limit = 0x7fffffffull;
+
+// Makes `device` current for the scope and restores the caller's device.
+class DeviceGuard {
+   public:
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != device) ok_ = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_) (void)hipSetDevice(prev_);
+    }
+    bool ok() const { return ok_; }
+
+   private:
+    int prev_ = -1;
+    bool ok_ = true;
+};
+
+inline uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+
+inline int env_int(const char *name, int fallback) {
+    const char *v = std::getenv(name);
+    if (!v || !*v) return fallback;
+    return std::atoi(v);
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline bool overlaps(const void *a, uint64_t a_bytes, const void *b, uint64_t b_bytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a_bytes && b_bytes && a0 < b0 + b_bytes && b0 < a0 + a_bytes;
+}
+
+inline vo_status device_status(const char *op, hipError_t err) {
+    if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
+    clear_error();
+    return VO_OK;
+}
+
+enum MetaKind { kNone = 0, kPrefill = 1, kDecode = 2, kSlots = 3 };
+
+// A row's last, shorter split in the decode work order (keys < split size).
+struct TailItem {
+    uint32_t keys, row, split;
+};
+
+}  // namespace vo
+
+struct vo_kv_pool {
+    vo_kv_layout layout{};
+    int device = 0;
+    int num_cus = 256;
+    uint16_t *base = nullptr;   // [layers][K|V][layer_elems] bf16
+    uint64_t layer_elems = 0;   // elements of one layer's K (or V)
+    uint64_t bytes = 0;
+
+    vo::kernels::PoolLayer layer(uint64_t l) const {
+        vo::kernels::PoolLayer p;
+        p.k = base + l * 2 * layer_elems;
+        p.v = p.k + layer_elems;
+        p.kv_heads = static_cast<uint32_t>(layout.kv_heads);
+        p.head_dim = static_cast<uint32_t>(layout.head_dim);
+        p.block_size = static_cast<uint32_t>(layout.block_size);
+        return p;
+    }
+};
+
+struct vo_step_meta {
+    int device = 0;
+    int num_cus = 256;
+    uint64_t pool_block_size = 0;
+    uint64_t kv_heads = 0;
+    uint64_t head_dim = 0;
+
+    uint64_t max_seqs = 0, max_rows = 0, max_entries = 0, max_heads = 0, max_parts = 0;
+
+    vo::MetaKind kind = vo::kNone;
+    uint64_t block_size = 0;
+    uint64_t num_seqs = 0;
+    uint64_t num_rows = 0;
+
+    // Host copies, for validation with the reference's error semantics.
+    std::vector<uint64_t> table_off;    // [S+1]
+    std::vector<uint32_t> tables;       // [entries]
+    std::vector<uint32_t> slots;        // [T] as given
+    std::vector<uint32_t> row_seq;      // [T]
+    std::vector<uint32_t> row_num_keys; // [T]
+    uint32_t max_block = 0;             // max table entry (0 if none)
+    uint32_t max_slot = 0;              // max slot (0 if none)
+    bool has_positions = false;         // positions were uploaded (RoPE needs them)
+    std::vector<uint32_t> positions;    // [T] when uploaded
+    uint32_t max_position = 0;          // largest position (0 if none)
+
+    // Device buffer and pinned staging of the same size.
+    uint8_t *d_buf = nullptr;
+    uint8_t *h_stage = nullptr;
+    uint64_t buf_bytes = 0;
+    hipEvent_t copy_done = nullptr;
+    bool copy_pending = false;
+
+    // Split-K partials (fp32).
+    float *d_part_acc = nullptr;
+    float *d_part_ml = nullptr;
+
+    vo::kernels::MetaView view{};
+    const uint32_t *d_write_slots = nullptr;  // slots with superseded rows = kSkipSlot
+    vo::kernels::WritePlan write_plan{};      // runs of consecutive slots inside one block
+    vo::kernels::DecodePlan plan{};
+    bool decode_planned = false;
+    std::vector<vo::TailItem> tail_items;  // scratch of plan_decode (capacity kept across steps)
+    std::vector<uint8_t> block_seen;   // scratch of plan_decode: one byte per physical block
+    std::vector<uint64_t> seq_keys;    // scratch of plan_decode: keys read per sequence
+    std::vector<uint32_t> decode_rows; // rows of a prefill step planned on the decode kernel
+    vo::kernels::PrefillPlan prefill_plan{};
+    bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
+
+    // Rows the LM head reads (PrefillMeta::last_rows, paged.rs:153-159): each
+    // sequence's last row for a prefill upload, every row for a decode upload.
+    const uint32_t *d_last_rows = nullptr;  // [num_seqs]
+    bool last_rows_ok = false;              // false: a sequence has no rows
+
+    // Token ids of the step (Llama::prefill/decode `tokens`, model.rs:221-243),
+    // uploaded apart from the metadata: host copy for embed's check, device
+    // copy for the kernel, pinned staging for the copy.
+    std::vector<uint32_t> tokens;
+    uint32_t *d_tokens = nullptr;   // [max_rows]
+    uint32_t *h_tokens = nullptr;   // [max_rows], pinned
+    hipEvent_t tokens_done = nullptr;
+    bool tokens_pending = false;
+    bool has_tokens = false;
+};
+
+struct vo_rope_table {
+    int device = 0;
+    uint64_t head_dim = 0, half = 0, max_len = 0;
+    float *d_cos = nullptr;  // [max_len][half]
+    float *d_sin = nullptr;
+};
