@@ -293,6 +293,93 @@ def bench_mixed(vo, W, orc, args):
     }
 
 
+def bench_model(vo, W, orc, args):
+    """one full mixed continuous-batching step of a
+    random-init Llama-3-8B-shaped model (32 layers, hidden 4096, 32q/8kv heads,
+    head_dim 128, FFN 14336, vocab 128256, theta 500000), bf16 weights
+    ~ N(0, 0.02) drawn on the GPU: 256 decode sequences (context lognormal,
+    median 1024, clipped to [128, 8192]) plus two 512-token prefill chunks in
+    one step (1280 rows).  One step = Llama::forward (model.rs:269-356) through
+    the C ABI: embed, 32 x (rmsnorm, QKV GEMM, fused RoPE + cache write,
+    attention, O GEMM + residual, rmsnorm, gate/up GEMM, silu_mul, down GEMM +
+    residual), last-row rmsnorm, LM head GEMM, argmax with its host copy."""
+    import importlib
+    import torch
+    M = importlib.import_module("vllm_oxide_amd.model")
+    cfg = W.llama3_8b_config(args.model_layers)
+    hd, H, F, V = cfg.head_dim, cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qd, kvd = cfg.num_attention_heads * hd, cfg.num_key_value_heads * hd
+    ctx, new = W.cfg4_attention_lens()
+    S, T = len(ctx), int(np.sum(new))
+    backend = vo.HipBackend(device=0, max_seqs=S, max_rows=W.FILL_ROWS,
+                            max_table_entries=30000, max_query_heads=cfg.num_attention_heads)
+    num_blocks = 30000
+    wl = W.build(vo, backend, kind="prefill", heads=cfg.num_attention_heads,
+                 kv_heads=cfg.num_key_value_heads, head_dim=hd, block_size=16,
+                 num_blocks=num_blocks, context_lens=ctx, num_new=new, seed=4,
+                 num_layers=cfg.num_hidden_layers, fill_layers=range(cfg.num_hidden_layers),
+                 keep_host=False)
+    del wl.ctx_kv[:]
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(44)
+
+    def nrm(o, i):
+        return (torch.randn((o, i), generator=gen, device="cuda:0", dtype=torch.float32)
+                * 0.02).to(torch.bfloat16)
+
+    ones = torch.ones(H, dtype=torch.bfloat16, device="cuda:0")
+    weights = dict(embed=nrm(V, H), final_norm=ones, layers=[
+        dict(attn_norm=ones, wq=nrm(qd, H), wk=nrm(kvd, H), wv=nrm(kvd, H), wo=nrm(H, qd),
+             mlp_norm=ones, w_gate=nrm(F, H), w_up=nrm(F, H), w_down=nrm(H, F))
+        for _ in range(cfg.num_hidden_layers)])
+    mc = M.ModelConfig(H, F, cfg.num_hidden_layers, cfg.num_attention_heads,
+                       cfg.num_key_value_heads, V, cfg.max_position_embeddings,
+                       cfg.rms_norm_eps, cfg.rope_theta, dict(cfg.rope_scaling))
+    ec = M.EngineConfig(max_batch_tokens=T, max_seqs=S, max_model_len=8192 + 1024,
+                        block_size=16, num_blocks=num_blocks)
+    model = M.Llama(backend, mc, ec, weights)
+    del weights
+    torch.cuda.empty_cache()
+    tokens = [int(t) for t in np.random.default_rng(4).integers(0, V, T)]
+
+    def step(i):
+        model.prefill(wl.pool, tokens, wl.meta)
+
+    sec = time_steps(torch, step, args.steps, args.warmup)
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    prof_steps = max(3, min(args.steps, 10))
+    time_steps(torch, step, prof_steps, 0)
+    vo.enable_profiling(False)
+    prof = vo.profile()
+    L = cfg.num_hidden_layers
+    gemm_flops = (L * 2 * T * H * (qd + 2 * kvd + qd + 2 * F + F) + 2 * S * H * V)
+    mm = prof.get("matmul", {"avg_ms": float("nan"), "calls": 0})
+    mm_ms_step = mm["avg_ms"] * mm["calls"] / prof_steps
+    achieved = gemm_flops / (mm_ms_step * 1e-3) / 1e12
+    return {
+        "metric": "full mixed continuous-batching step tokens/s (Llama-3-8B shape, cfg4), 1 GPU",
+        "value": round(T / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0, 0.02), random token ids and cached K/V)",
+        "config": {"workload": f"cfg4: Llama-3-8B shape, {L} layers, 256 decode (lognormal median "
+                               "1024, sigma 1, clip [128, 8192], seed 4) + 2 x 512-token "
+                               "prefill chunks (ctx 0, 1536); 1280 rows; block 16",
+                   "step": "Llama::forward through the C ABI incl. argmax host copy"},
+        "decode_tokens_per_s": round(256 / sec, 1),
+        "roofline": {"bound": "mfma", "kernel": "hipBLASLt GEMMs (sum)",
+                     "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "gemm_tflop_per_step": round(gemm_flops / 1e12, 3),
+        "kernels_ms_per_step": {k: round(v["avg_ms"] * v["calls"] / prof_steps, 4)
+                                for k, v in sorted(prof.items(),
+                                                   key=lambda kv: -kv[1]["avg_ms"] * kv[1]["calls"])},
+        "cpu_baseline": None,
+    }
+
+
 def bench_rope_write(vo, W, orc, args):
     """The layer step before attention (model.rs:307-311): rope(q); rope(k);
     write_kv(k, v) as three launches, against the fused rope_write_kv, at the
@@ -338,7 +425,10 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=2, help="pool layers to rotate over")
-    ap.add_argument("--config", default="cfg2", choices=["cfg2", "cfg3", "cfg4a", "cfg5", "rope", "all"])
+    ap.add_argument("--config", default="cfg2",
+                    choices=["cfg2", "cfg3", "cfg4", "cfg4a", "cfg5", "rope", "all"])
+    ap.add_argument("--model-layers", type=int, default=32,
+                    help="cfg4: decoder layers (32 = Llama-3-8B)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
@@ -388,6 +478,8 @@ def main():
         lines.append(bench_prefill(vo, W, orc, args))
     if args.config in ("cfg4a", "all"):
         lines.append(bench_mixed(vo, W, orc, args))
+    if args.config in ("cfg4", "all"):
+        lines.append(bench_model(vo, W, orc, args))
     if args.config in ("rope", "all"):
         lines.append(bench_rope_write(vo, W, orc, args))
     for line in lines:

@@ -15,10 +15,12 @@
 // -- is the one bound; otherwise libhipblaslt.so.1 from the loader path.
 // Nothing else in the library depends on it.
 //
-// Algorithm choice: hipBLASLt's heuristic, once per (rows, N, K, out type,
-// accumulate), cached with its descriptors; no per-call allocation (the
-// workspace is allocated at creation), so calls may be captured in a HIP
-// graph.  Shapes whose rows are not whole 16-byte words go to a generic
+// Algorithm choice, once per (rows, N, K, out type, accumulate), cached with
+// its descriptors: hipBLASLt's first heuristic choice, or with VO_GEMM_TUNE=1
+// the fastest of its candidates timed on the first call's operands (on the
+// Llama-3-8B step shapes the two measured the same).
+// Later calls allocate nothing (the workspace is allocated at creation) and
+// may be captured in a HIP graph; the first call of a shape may not.  Shapes whose rows are not whole 16-byte words go to a generic
 // kernel (kernels/layer_ops.hip).
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
@@ -106,8 +108,12 @@ using PlanKey = std::tuple<uint64_t, uint64_t, uint64_t, int32_t, int32_t>;
 
 }  // namespace
 
+constexpr int kTuneCandidates = 16;  // heuristic candidates timed per shape
+constexpr int kTuneRepeats = 5;      // timed runs per candidate
+
 struct vo_gemm {
     int device = 0;
+    bool tune = false;  // time the heuristic's candidates per shape (VO_GEMM_TUNE=1: on)
     hipblasLtHandle_t lt = nullptr;
     void *workspace = nullptr;
     uint64_t workspace_bytes = 0;
@@ -129,10 +135,62 @@ void destroy_plan(const LtApi &api, Plan &p) {
     p = Plan{};
 }
 
+// Times the heuristic's candidates on the call's own operands (beta = 0,
+// into a scratch output, so an accumulating call's output is untouched) and
+// keeps the fastest.  Runs once per shape, at its first call: it allocates
+// and waits, so that call must not be under stream capture.  Candidates that
+// fail to run are skipped; if every timing fails the heuristic's first
+// choice stays.
+void tune_plan(vo_gemm *g, const LtApi &api, const void *x, const void *w, uint64_t rows,
+               uint64_t n, int32_t out_dtype, const hipblasLtMatmulHeuristicResult_t *cand,
+               int count, hipStream_t stream, Plan &p) {
+    void *scratch = nullptr;
+    const uint64_t bytes = rows * n * (out_dtype == VO_DTYPE_F32 ? 4 : 2);
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (hipMalloc(&scratch, bytes) != hipSuccess) return;
+    if (hipEventCreate(&t0) != hipSuccess || hipEventCreate(&t1) != hipSuccess) {
+        if (t0) (void)hipEventDestroy(t0);
+        (void)hipFree(scratch);
+        return;
+    }
+    const float alpha = 1.0f, beta = 0.0f;
+    float best = 0.0f;
+    int best_i = -1;
+    for (int i = 0; i < count; ++i) {
+        if (cand[i].state != HIPBLAS_STATUS_SUCCESS || cand[i].workspaceSize > g->workspace_bytes)
+            continue;
+        auto run = [&]() {
+            return api.matmul(g->lt, p.desc, &alpha, w, p.a, x, p.b, &beta, scratch, p.c, scratch,
+                              p.c, &cand[i].algo, cand[i].workspaceSize ? g->workspace : nullptr,
+                              cand[i].workspaceSize, stream);
+        };
+        if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up
+        bool ok = hipEventRecord(t0, stream) == hipSuccess;
+        for (int r = 0; ok && r < kTuneRepeats; ++r) ok = run() == HIPBLAS_STATUS_SUCCESS;
+        ok = ok && hipEventRecord(t1, stream) == hipSuccess && hipEventSynchronize(t1) == hipSuccess;
+        float ms = 0.0f;
+        if (!ok || hipEventElapsedTime(&ms, t0, t1) != hipSuccess) continue;
+        if (best_i < 0 || ms < best) {
+            best = ms;
+            best_i = i;
+        }
+    }
+    (void)hipStreamSynchronize(stream);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    (void)hipFree(scratch);
+    if (best_i >= 0) {
+        p.algo = cand[best_i].algo;
+        p.workspace = cand[best_i].workspaceSize;
+    }
+}
+
 // Builds the descriptors of one problem and asks the heuristic for its best
-// algorithm that fits the workspace.
+// algorithms that fit the workspace; with tuning on, the fastest of them on
+// this call's operands is kept.
 vo_status make_plan(vo_gemm *g, const LtApi &api, uint64_t rows, uint64_t n, uint64_t k,
-                    int32_t out_dtype, Plan &p) {
+                    int32_t out_dtype, const void *x, const void *w, hipStream_t stream,
+                    Plan &p) {
     const char *op = "matmul";
     const hipDataType out_t = out_dtype == VO_DTYPE_F32 ? HIP_R_32F : HIP_R_16BF;
     hipblasStatus_t st = api.desc_create(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
@@ -151,10 +209,11 @@ vo_status make_plan(vo_gemm *g, const LtApi &api, uint64_t rows, uint64_t n, uin
     if (st != HIPBLAS_STATUS_SUCCESS) return lt_fail(op, "hipblasLtMatmulPreferenceCreate", st);
     const uint64_t ws = g->workspace_bytes;
     st = api.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-    hipblasLtMatmulHeuristicResult_t result[1];
+    hipblasLtMatmulHeuristicResult_t result[kTuneCandidates];
     int returned = 0;
+    const int want = g->tune ? kTuneCandidates : 1;
     if (st == HIPBLAS_STATUS_SUCCESS)
-        st = api.heuristic(g->lt, p.desc, p.a, p.b, p.c, p.c, pref, 1, result, &returned);
+        st = api.heuristic(g->lt, p.desc, p.a, p.b, p.c, p.c, pref, want, result, &returned);
     api.pref_destroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS) return lt_fail(op, "hipblasLtMatmulAlgoGetHeuristic", st);
     if (returned < 1)
@@ -163,6 +222,7 @@ vo_status make_plan(vo_gemm *g, const LtApi &api, uint64_t rows, uint64_t n, uin
                                         std::to_string(k) + "]^T");
     p.algo = result[0].algo;
     p.workspace = result[0].workspaceSize;
+    if (returned > 1) tune_plan(g, api, x, w, rows, n, out_dtype, result, returned, stream, p);
     return VO_OK;
 }
 
@@ -180,6 +240,7 @@ extern "C" int32_t vo_gemm_create(int32_t device, uint64_t workspace_bytes, vo_g
     if (!g) return fail_argument(op, "out of host memory");
     g->device = device;
     g->workspace_bytes = workspace_bytes;
+    g->tune = env_int("VO_GEMM_TUNE", 0) != 0;
     hipblasStatus_t st = api.create(&g->lt);
     if (st != HIPBLAS_STATUS_SUCCESS) {
         delete g;
@@ -253,7 +314,8 @@ extern "C" int32_t vo_matmul(vo_gemm *g, const void *x, uint64_t rows, uint64_t 
         auto it = g->plans.find(key);
         if (it == g->plans.end()) {
             Plan p;
-            if (vo_status rc = make_plan(g, api, rows, out_features, in_features, out_dtype, p)) {
+            if (vo_status rc = make_plan(g, api, rows, out_features, in_features, out_dtype, x, weight,
+                                          static_cast<hipStream_t>(stream), p)) {
                 destroy_plan(api, p);
                 return rc;
             }
