@@ -59,6 +59,8 @@
 // Roofline: bf16 MFMA.  Algorithmic FLOPs = sum over rows of (keys) * heads *
 // 4 * head_dim (Q.K^T and P.V, causal-aware).
 #include <cmath>
+#include <cstdlib>
+#include <string>
 #include <type_traits>
 
 #include "vo_device.hpp"
@@ -343,6 +345,309 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2)))
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same kernel with the KV tiles staged by LDS DMA (gfx950
+// global_load_lds_dwordx4: each lane's 16 bytes go from its own global
+// address straight into LDS at base + 16 * lane) through a ring of three LDS
+// stages, so the tile two ahead is in flight while this one is computed and
+// no registers or ds_write instructions carry the staging.
+//
+// A stage keeps the pool's own tile layout, block after block: K as
+// [4 blocks][head_dim/32][16 keys][32 dims] and V as [4 blocks][head_dim]
+// [16 keys], so every DMA instruction copies 1 KiB of one (block, KV head)
+// tile.  A DMA instruction cannot pad, so bank conflicts are avoided by a
+// permutation of the 16-byte units inside each 256-byte line, chosen per
+// lane on the global side: the unit U of a block tile is stored at
+//   K: U ^ ((U >> 4) & 3)        V: U ^ ((U >> 4) & 1).
+// A ds_read_b128 phase (16 lanes) of the Q.K^T A operand reads 16 keys of
+// one block at one (chunk, 8-dim unit): U = 64 ch + 4 key + s, which the K
+// map spreads over all 16 units of a line; the P.V A operand reads 16 dims
+// at one 8-key half: U = 2 dim + half, which the V map spreads likewise.
+// Both maps leave the per-lane read address independent of the MFMA step,
+// so the steps are immediate offsets.
+//
+// The block table of the item's sequence is copied to LDS first, so the
+// per-tile block ids are LDS reads: no global load joins the DMA
+// instructions in the vector-memory counter.  Stage s of tile t is read
+// after an explicit s_waitcnt that leaves only the wave's newest DMA
+// instructions (tile t + 1's) outstanding, then a barrier; compiler-only
+// fences keep LDS reads on their side of it.
+constexpr uint32_t kTableLds = 4096;  // block-table entries the DMA kernel stages
+
+template <int HD, int W>
+struct DmaShape {
+    static constexpr int BT = HD * kBS * 2;       // bytes of one (block, KV head) tile
+    static constexpr int IPB = BT / 1024;         // DMA instructions per block tile
+    static constexpr int KBYTES = 4 * BT;
+    static constexpr int STAGE = 2 * KBYTES;      // K then V
+    static constexpr int NK = 4 * IPB;            // K DMA instructions per KV tile
+    static constexpr int DPW = 2 * NK / W;        // per wave: DPW/2 for K, DPW/2 for V
+    static_assert((2 * NK) % W == 0 && DPW % 2 == 0 && DPW <= 15, "DMA split");
+};
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), then a workgroup barrier.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                          uint32_t i) {
+    return i < 2 ? (i == 0 ? a : b) : (i == 2 ? c : d);
+}
+
+template <int HD, int G, int R>
+__global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2))) void prefill_dma_kernel(
+    const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
+    const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
+    const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
+    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2) {
+    constexpr int W = G * R;
+    constexpr int HALVES = kQT / (kRG * R);
+    using D = DmaShape<HD, W>;
+    constexpr int KS = HD / 16;
+    constexpr int DT = HD / 32;
+    constexpr int DPW = D::DPW;
+    constexpr uint32_t kTile = kBS * HD;
+
+    __shared__ uint32_t tbl[kTableLds];
+    __shared__ __align__(1024) uint8_t st0[D::STAGE];
+    __shared__ __align__(1024) uint8_t st1[D::STAGE];
+    __shared__ __align__(1024) uint8_t st2[D::STAGE];
+
+    const uint32_t kvh = blockIdx.x % kv_heads;
+    const uint32_t rest = blockIdx.x / kv_heads;
+    const uint32_t item = rest / HALVES;
+    const uint32_t wg_row0 = (rest % HALVES) * (kRG * R);
+    const uint32_t item_rows = work[4 * item + 1];
+    if (wg_row0 >= item_rows) return;  // whole workgroup, before any barrier
+    const uint32_t row_begin = work[4 * item] + wg_row0;
+    const uint32_t nrows = min(item_rows - wg_row0, static_cast<uint32_t>(kRG * R));
+    const uint32_t p_min = work[4 * item + 2] + wg_row0;
+    const uint32_t seq = work[4 * item + 3];
+    const uint32_t p_max = p_min + nrows - 1;
+    const uint32_t n_tiles = p_max / kKT + 1;
+    const uint32_t nblk = p_max / kBS + 1;  // <= kTableLds (checked by the launcher)
+    const uint32_t *table = tables + table_off[seq];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t head = wave % G;
+    const uint32_t rg = wave / G;
+    const uint32_t c = lane & 31;
+    const uint32_t gl = lane >> 5;
+    const uint32_t qhead = kvh * G + head;
+    const uint32_t lr = kRG * rg + c;
+    const bool row_ok = lr < nrows;
+    const uint32_t p_row = p_min + lr;
+    const uint32_t wp_min = p_min + kRG * rg;
+    const uint32_t wp_max = min(wp_min + kRG - 1, p_max);
+
+    for (uint32_t i = tid; i < nblk; i += 64 * W) tbl[i] = table[i];
+
+    bf16x8 qv[KS];
+    {
+        const uint16_t *qp =
+            q + (static_cast<uint64_t>(row_begin + lr) * num_heads + qhead) * HD + 8 * gl;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+            qv[kk] = row_ok ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 16 * kk))
+                            : bf16x8{};
+    }
+    wait_barrier<0>();  // the table copy
+
+    // DMA sources: wave instruction i is K instruction i * W + wave for
+    // i < DPW/2, V instruction (i - DPW/2) * W + wave after; instruction qi
+    // copies 1 KiB number qi % IPB of block qi / IPB.  Lane L writes physical
+    // unit P = 64 (qi % IPB) + L of the block tile and reads logical unit U.
+    uint32_t dma_off[DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+        const uint32_t qi = (i % (DPW / 2)) * W + wave;
+        const uint32_t P = 64 * (qi % D::IPB) + lane;
+        const uint32_t U = i < DPW / 2 ? P ^ ((P >> 4) & 3u) : P ^ ((P >> 4) & 1u);
+        dma_off[i] = U * 8;
+    }
+    auto dma_tile = [&](uint8_t *stage, uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) {
+            const bool is_k = i < DPW / 2;
+            const uint32_t qi = (i % (DPW / 2)) * W + wave;
+            const uint32_t blk = pick4(b0, b1, b2, b3, qi / D::IPB);
+            const uint16_t *pool = is_k ? k_pool : v_pool;
+            const uint16_t *src = pool + (static_cast<uint64_t>(blk) * kv_heads + kvh) * kTile + dma_off[i];
+            uint8_t *dst = stage + (is_k ? 0 : D::KBYTES) + qi * 1024;
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+        }
+    };
+    auto blk_of = [&](uint32_t t, int b) { return tbl[min(4 * t + b, nblk - 1)]; };
+
+    float m_run = 0.0f;
+    float l_run = 0.0f;
+    floatx16 o_acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
+
+    // LDS read offsets.  K: A-row c reads key kp = key_perm(c) of block kp/16
+    // (+2 blocks for the second 32-key half), chunk kk/2, unit 2(kk%2) + gl,
+    // stored at unit ^ ((kp % 16) >> 2).  V: A-row c reads dim 32 dt + c of
+    // block j, half gl, stored at half ^ ((c >> 3) & 1).
+    const uint32_t kp = key_perm(c);
+    const uint32_t kx = ((kp & 15) >> 2) & 3;
+    const uint32_t k_rd0 = (kp / 16) * D::BT + (kp & 15) * 64 + 16 * (gl ^ kx);
+    const uint32_t k_rd1 = (kp / 16) * D::BT + (kp & 15) * 64 + 16 * ((gl ^ kx) ^ 2);
+    const uint32_t v_rd = D::KBYTES + c * 32 + 16 * (gl ^ ((c >> 3) & 1));
+
+    uint32_t n0, n1, n2, n3;  // block ids of tile t + 2 while step t runs
+    // The stage read and the stage filled are passed as restrict pointers, so
+    // the compiler knows this step's DMA does not write what it reads (it
+    // then inserts no wait for that DMA before the reads).
+    auto body = [&](auto first_c, uint32_t t, const uint8_t *__restrict__ tile,
+                    uint8_t *__restrict__ ahead) __attribute__((always_inline)) {
+        constexpr bool first = decltype(first_c)::value;
+        // Every step issues its DMA, past the last tile too (block ids clamp
+        // to the table's last entry), so that every step has the same number
+        // of DMA instructions in flight and the compiler's wait tracking
+        // stays exact through the loop.
+        dma_tile(ahead, n0, n1, n2, n3);
+        n0 = blk_of(t + 3, 0);
+        n1 = blk_of(t + 3, 1);
+        n2 = blk_of(t + 3, 2);
+        n3 = blk_of(t + 3, 3);
+        const uint32_t j0 = t * kKT;
+        if (wp_min >= nrows + p_min || j0 > wp_max) goto staged;
+        {
+        floatx16 s0 = {}, s1 = {};
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
+            const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(tile + off);
+            const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * D::BT);
+            s0 = mfma32x32x16(a0, qv[kk], s0);
+            s1 = mfma32x32x16(a1, qv[kk], s1);
+        }
+
+        float sc[32];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = s0[r];
+            sc[16 + r] = s1[r];
+        }
+        if (j0 + kKT - 1 > wp_min) {
+#pragma unroll
+            for (int r = 0; r < 32; ++r) {
+                const uint32_t key = j0 + 32 * (r >> 4) + 16 * ((r >> 3) & 1) + 8 * gl + (r & 7);
+                sc[r] = (key <= p_row) ? sc[r] : -INFINITY;
+            }
+        }
+        float mx = sc[0];
+#pragma unroll
+        for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mt = mx * scale_log2;
+        if constexpr (first) {
+            m_run = mt;
+        } else if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazyLog2) != 0) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
+            m_run = m_new;
+        }
+        const float nm = -m_run;
+#pragma unroll
+        for (int r = 0; r < 32; ++r) sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, nm));
+
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bf16x8 pb_hi, pb_lo;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float p = sc[16 * (j >> 1) + 8 * (j & 1) + i];
+                const __bf16 hi = static_cast<__bf16>(p);
+                pb_hi[i] = hi;
+                if constexpr (first) {
+                    pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+                    l_run += p;
+                }
+            }
+            if constexpr (!first) l_run = sum8(pb_hi, l_run);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const bf16x8 a = *reinterpret_cast<const bf16x8 *>(tile + v_rd + j * D::BT + dt * 1024);
+                if constexpr (first) o_acc[dt] = mfma32x32x16(a, pb_lo, o_acc[dt]);
+                o_acc[dt] = mfma32x32x16(a, pb_hi, o_acc[dt]);
+            }
+        }
+        }
+    staged:
+        // Tile t + 1 must have landed; tile t + 2 (this step's DMA) may fly on.
+        wait_barrier<DPW>();
+    };
+    auto step = [&](auto buf_c, auto first_c, uint32_t t) {
+        constexpr int buf = decltype(buf_c)::value;
+        if constexpr (buf == 0) body(first_c, t, st0, st2);
+        else if constexpr (buf == 1) body(first_c, t, st1, st0);
+        else body(first_c, t, st2, st1);
+    };
+
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    using First = std::integral_constant<bool, true>;
+    using Rest = std::integral_constant<bool, false>;
+
+    dma_tile(st0, blk_of(0, 0), blk_of(0, 1), blk_of(0, 2), blk_of(0, 3));
+    dma_tile(st1, blk_of(1, 0), blk_of(1, 1), blk_of(1, 2), blk_of(1, 3));
+    n0 = blk_of(2, 0);
+    n1 = blk_of(2, 1);
+    n2 = blk_of(2, 2);
+    n3 = blk_of(2, 3);
+    wait_barrier<DPW>();
+    step(B0{}, First{}, 0);
+    for (uint32_t t = 1; t < n_tiles; t += 3) {
+        step(B1{}, Rest{}, t);
+        if (t + 1 >= n_tiles) break;
+        step(B2{}, Rest{}, t + 1);
+        if (t + 2 >= n_tiles) break;
+        step(B0{}, Rest{}, t + 2);
+    }
+    // The DMA of the tiles past the end is still in flight: it must land
+    // before the workgroup's LDS is released.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (!row_ok) return;
+    const float inv = 1.0f / l_run;
+    uint16_t *op = out + (static_cast<uint64_t>(row_begin + lr) * num_heads + qhead) * HD + 4 * gl;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            u32x2 packed;
+            packed[0] = f32_to_bf16_bits(o_acc[dt][4 * r4] * inv) |
+                        (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[dt][4 * r4 + 1] * inv)) << 16);
+            packed[1] = f32_to_bf16_bits(o_acc[dt][4 * r4 + 2] * inv) |
+                        (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[dt][4 * r4 + 3] * inv)) << 16);
+            *reinterpret_cast<u32x2 *>(op + 32 * dt + 8 * r4) = packed;
+        }
+    }
+}
+
+// VO_PREFILL_STAGING=regs selects the register-staged kernel above (A/B).
+bool prefill_use_dma() {
+    static const bool dma = [] {
+        const char *v = std::getenv("VO_PREFILL_STAGING");
+        return !(v && std::string(v) == "regs");
+    }();
+    return dma;
+}
+
 template <int HD, int G>
 hipError_t launch_g(const PoolLayer &pool, const MetaView &meta, const PrefillPlan &plan,
                     const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
@@ -353,6 +658,19 @@ hipError_t launch_g(const PoolLayer &pool, const MetaView &meta, const PrefillPl
     const uint64_t grid = static_cast<uint64_t>(plan.num_items) * HALVES * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("prefill_mfma", stream);
+    // The DMA kernel stages a sequence's whole block table in LDS, and its
+    // three 32 KiB stages at head_dim 128 leave room for one workgroup per
+    // CU, which takes 8 wavefronts to fill the SIMDs.
+    constexpr bool dma_shape = HD == 64 || G * R == 8;
+    if constexpr (dma_shape) {
+        if (prefill_use_dma() && plan.max_keys <= kTableLds * kBS) {
+            hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
+                               dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
+                               meta.table_off, meta.tables, plan.work, q, out, num_heads,
+                               scale_log2);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((prefill_mfma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
                        dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
                        meta.tables, plan.work, q, out, num_heads, scale_log2);

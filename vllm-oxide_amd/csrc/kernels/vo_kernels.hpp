@@ -170,6 +170,7 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
 struct PrefillPlan {
     const uint32_t *work;  // [num_items][4]: (first row, rows, position of first row, sequence)
     uint32_t num_items;
+    uint32_t max_keys;     // largest key count of any row (position + 1) in the plan
 };
 
 // True when the MFMA prefill kernel covers this shape.

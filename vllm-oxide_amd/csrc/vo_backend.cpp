@@ -460,6 +460,9 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
     }
     m->prefill_plan.work = dp;
     m->prefill_plan.num_items = static_cast<uint32_t>(items.size());
+    uint32_t max_keys = 0;
+    for (const Item &it : items) max_keys = std::max(max_keys, it.pos + it.rows);
+    m->prefill_plan.max_keys = max_keys;
     if (!m->decode_rows.empty())
         if (vo_status rc = plan_decode_rows(m, pk, &m->decode_rows)) return rc;
     m->prefill_planned = true;
