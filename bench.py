@@ -380,6 +380,86 @@ def bench_model(vo, W, orc, args):
     }
 
 
+def bench_model_decode(vo, W, orc, args):
+    """Decode-only steps of the random-init Llama-3-8B-shaped model: S
+    sequences (context lognormal, median 1024, clipped to [128, 8192]) each
+    add one token per step; one step = Llama::decode through the C ABI,
+    argmax included.  Prints one line per batch size in --decode-batches."""
+    import importlib
+    import torch
+    M = importlib.import_module("vllm_oxide_amd.model")
+    cfg = W.llama3_8b_config(args.model_layers)
+    hd, H, F, V = cfg.head_dim, cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    qd, kvd = cfg.num_attention_heads * hd, cfg.num_key_value_heads * hd
+    batches = [int(b) for b in args.decode_batches.split(",")]
+    S_max = max(batches)
+    ctx, _ = W.cfg4_attention_lens(num_decode=S_max, chunk_ctx=())
+    backend = vo.HipBackend(device=0, max_seqs=S_max, max_rows=W.FILL_ROWS,
+                            max_table_entries=40000, max_query_heads=cfg.num_attention_heads)
+    num_blocks = int(sum(-(-(int(c) + 1) // 16) for c in ctx)) + 64
+    wl = W.build(vo, backend, kind="decode", heads=cfg.num_attention_heads,
+                 kv_heads=cfg.num_key_value_heads, head_dim=hd, block_size=16,
+                 num_blocks=num_blocks, context_lens=ctx, seed=5,
+                 num_layers=cfg.num_hidden_layers, fill_layers=range(cfg.num_hidden_layers),
+                 keep_host=False)
+    del wl.ctx_kv[:]
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(45)
+
+    def nrm(o, i):
+        return (torch.randn((o, i), generator=gen, device="cuda:0", dtype=torch.float32)
+                * 0.02).to(torch.bfloat16)
+
+    ones = torch.ones(H, dtype=torch.bfloat16, device="cuda:0")
+    weights = dict(embed=nrm(V, H), final_norm=ones, layers=[
+        dict(attn_norm=ones, wq=nrm(qd, H), wk=nrm(kvd, H), wv=nrm(kvd, H), wo=nrm(H, qd),
+             mlp_norm=ones, w_gate=nrm(F, H), w_up=nrm(F, H), w_down=nrm(H, F))
+        for _ in range(cfg.num_hidden_layers)])
+    mc = M.ModelConfig(H, F, cfg.num_hidden_layers, cfg.num_attention_heads,
+                       cfg.num_key_value_heads, V, cfg.max_position_embeddings,
+                       cfg.rms_norm_eps, cfg.rope_theta, dict(cfg.rope_scaling))
+    ec = M.EngineConfig(max_batch_tokens=S_max, max_seqs=S_max, max_model_len=8192 + 1024,
+                        block_size=16, num_blocks=num_blocks)
+    model = M.Llama(backend, mc, ec, weights)
+    del weights
+    torch.cuda.empty_cache()
+    lines = []
+    for S in batches:
+        meta = vo.DecodeMeta.new([vo.DecodeSeq(int(ctx[s]), wl.tables[s]) for s in range(S)], 16)
+        tokens = [int(t) for t in np.random.default_rng(S).integers(0, V, S)]
+
+        def step(i):
+            model.decode(wl.pool, tokens, meta)
+
+        sec = time_steps(torch, step, args.steps, args.warmup)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            model.enqueue(wl.pool, tokens, meta, False)
+        host = (time.perf_counter() - t0) / 5
+        torch.cuda.synchronize()
+        graph_ms = None
+        if args.graph:
+            graph = model.capture_decode(wl.pool, tokens, meta)
+            eager = model.decode(wl.pool, tokens, meta, want_logits=True)
+            replay = graph.run(tokens, meta, want_logits=True)
+            if replay.tokens != eager.tokens or not np.array_equal(replay.logits, eager.logits):
+                raise SystemExit(f"graph replay differs from the eager step at {S} sequences")
+            gsec = time_steps(torch, lambda i: graph.run(tokens, meta), args.steps, args.warmup)
+            graph_ms = round(gsec * 1e3, 3)
+            backend.step_meta(wl.pool).unfix_launch()
+        lines.append({
+            "metric": "Llama-3-8B-shape decode step, 1 GPU", "value": round(S / sec, 1),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(sec * 1e3, 3), "higher_is_better": True, "dtype": "bf16",
+            "data": "synthetic (random-init weights N(0, 0.02), random cached K/V)",
+            "config": {"workload": f"decode, {S} sequences, context lognormal median 1024 "
+                                   f"(seed 4), {cfg.num_hidden_layers} layers"},
+            "host_enqueue_ms_per_step": round(host * 1e3, 3),
+            "graph_ms_per_step": graph_ms,
+            "graph_tokens_per_s": round(S / (graph_ms * 1e-3), 1) if graph_ms else None})
+    return lines
+
+
 def bench_rope_write(vo, W, orc, args):
     """The layer step before attention (model.rs:307-311): rope(q); rope(k);
     write_kv(k, v) as three launches, against the fused rope_write_kv, at the
@@ -426,7 +506,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=2, help="pool layers to rotate over")
     ap.add_argument("--config", default="cfg2",
-                    choices=["cfg2", "cfg3", "cfg4", "cfg4a", "cfg5", "rope", "all"])
+                    choices=["cfg2", "cfg3", "cfg4", "cfg4a", "cfg5", "decode", "rope", "all"])
+    ap.add_argument("--decode-batches", default="1,16,64,256",
+                    help="--config decode: batch sizes (sequences per step)")
+    ap.add_argument("--graph", action="store_true",
+                    help="--config decode: also time the step replayed as a HIP graph")
     ap.add_argument("--model-layers", type=int, default=32,
                     help="cfg4: decoder layers (32 = Llama-3-8B)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -480,6 +564,8 @@ def main():
         lines.append(bench_mixed(vo, W, orc, args))
     if args.config in ("cfg4", "all"):
         lines.append(bench_model(vo, W, orc, args))
+    if args.config == "decode":
+        lines.extend(bench_model_decode(vo, W, orc, args))
     if args.config in ("rope", "all"):
         lines.append(bench_rope_write(vo, W, orc, args))
     for line in lines:

@@ -235,6 +235,25 @@ int32_t vo_step_meta_upload_decode(vo_step_meta *meta, uint64_t block_size, uint
                                    const uint64_t *row_seq, const uint64_t *row_num_keys,
                                    void *stream);
 
+/* Fixed launch shapes, so that a decode step can be recorded once as a HIP
+ * graph and replayed for later steps (no counterpart in the reference; for
+ * engines that capture the decode step to take the per-launch host cost out
+ * of small-batch decoding).  Takes the last upload, which must be a decode
+ * step of S sequences, and uploads it again in a layout where every array
+ * has a fixed device address, sized for S sequences, the current table
+ * entries + entry_headroom and the current split-K work items +
+ * work_headroom; the decode kernels are then launched for that many work
+ * items and S reduce rows and read the step's own counts from the device.
+ * While fixed, every launch of a decode step through this meta has the same
+ * arguments and grid, and vo_step_meta_upload_decode accepts only steps that
+ * fit (else VO_ERR_SHAPE / VO_ERR_CAPACITY with nothing changed: unfix,
+ * upload, fix and record again); prefill and slot uploads are refused.  The
+ * first call of each GEMM shape (vo_matmul) must happen before recording. */
+int32_t vo_step_meta_fix_launch(vo_step_meta *meta, uint64_t work_headroom,
+                                uint64_t entry_headroom, void *stream);
+/* Back to packed uploads from the next upload on. */
+int32_t vo_step_meta_unfix_launch(vo_step_meta *meta);
+
 /* Upload only a slot list, for write_kv calls whose slots are not a step's
  * slot mapping (the reference's tests write ad-hoc ranges, cpu/tests.rs:210-230). */
 int32_t vo_step_meta_upload_slots(vo_step_meta *meta, const uint32_t *slots, uint64_t num_slots,

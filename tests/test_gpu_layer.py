@@ -415,3 +415,42 @@ def test_batch_checks(vo, M, gpu_backend):
     assert (e.value.value, e.value.limit) == (65, 64)
     with pytest.raises(vo.ShapeError):
         m.prefill(kv, W.ref_prompt(5, 0), vo.PrefillMeta.new([vo.PrefillSeq(0, 6, table)], 4))
+
+
+def test_decode_graph_replays_equal_eager_steps(vo, M, gpu_backend):
+    """A decode step recorded as a HIP graph (fixed launch shapes) and
+    replayed for 16 later steps gives bitwise the eager step's logits and ids;
+    eager work and syncs run between the replays.  Block tables grow as the
+    engine's do (each step passes the blocks its keys need); a step whose
+    table outgrows the fixed capacity is refused (CapacityError) and runs
+    after recording again."""
+    cfg, w, prompts, tables, _ = _cfg1_setup(seed=4)
+    lens = [len(p) for p in prompts]
+    ga, kva = _gpu_model(vo, M, gpu_backend, cfg, w, 64, 16)
+    gb, kvb = _gpu_model(vo, M, gpu_backend, cfg, w, 64, 16)
+    pm = vo.PrefillMeta.new([vo.PrefillSeq(0, n, t) for n, t in zip(lens, tables)], 16)
+    a = ga.prefill(kva, sum(prompts, []), pm)
+    b = gb.prefill(kvb, sum(prompts, []), pm)
+    assert a.tokens == b.tokens
+    toks, ctx = a.tokens, list(lens)
+    graph = None
+    refits = 0
+    for step in range(16):
+        meta = vo.DecodeMeta.new([vo.DecodeSeq(c, t[:(c + 16) // 16]) for c, t in zip(ctx, tables)],
+                                 16)
+        _say(f"graph decode step {step}")
+        want = ga.decode(kva, toks, meta, want_logits=True)
+        if graph is None:
+            # no table headroom: the first block boundary forces a new recording
+            graph = gb.capture_decode(kvb, toks, meta, entry_headroom=0)
+        try:
+            got = graph.run(toks, meta, want_logits=True)
+        except vo.CapacityError:
+            refits += 1
+            graph = gb.capture_decode(kvb, toks, meta, entry_headroom=0)
+            got = graph.run(toks, meta, want_logits=True)
+        assert got.tokens == want.tokens, f"step {step}"
+        assert np.array_equal(got.logits, want.logits), f"step {step}"
+        toks, ctx = want.tokens, [c + 1 for c in ctx]
+    _say(f"graph decode: 16 steps bitwise equal, {refits} re-recordings")
+    assert refits >= 1

@@ -152,6 +152,8 @@ SIGNATURES = {
     "vo_qkv_rope_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _u64, _vp, _vp,
                                               _vp]),
     "vo_step_meta_upload_tokens": (ctypes.c_int32, [_vp, _u32p, _u64, _vp]),
+    "vo_step_meta_fix_launch": (ctypes.c_int32, [_vp, _u64, _u64, _vp]),
+    "vo_step_meta_unfix_launch": (ctypes.c_int32, [_vp]),
     "vo_embed": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp]),
     "vo_rmsnorm": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp, _vp]),
     "vo_rmsnorm_last_rows": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp,
@@ -520,6 +522,15 @@ class StepMeta:
         t = _u32(tokens) if len(tokens) else np.zeros(1, np.uint32)
         _check(lib.vo_step_meta_upload_tokens(self._h, _p32(t), len(tokens),
                                               _stream_ptr(stream)))
+
+    def fix_launch(self, work_headroom: int, entry_headroom: int, stream=None) -> None:
+        """vo_step_meta_fix_launch: the last upload (a decode step) again, in
+        fixed-launch layout, ready to be recorded as a graph."""
+        _check(lib.vo_step_meta_fix_launch(self._h, work_headroom, entry_headroom,
+                                           _stream_ptr(stream)))
+
+    def unfix_launch(self) -> None:
+        _check(lib.vo_step_meta_unfix_launch(self._h))
 
     def upload_slots(self, slots, stream=None) -> None:
         s = _u32(slots)

@@ -192,7 +192,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                      const uint32_t *__restrict__ row_info, uint32_t split_keys,
                      const uint16_t *__restrict__ q, uint16_t *__restrict__ out,
                      float *__restrict__ part_acc, float *__restrict__ part_ml, uint32_t num_heads,
-                     uint32_t group, float scale_log2) {
+                     uint32_t group, float scale_log2, const uint32_t *__restrict__ counts) {
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
     constexpr uint32_t kTile = kBS * HD;
@@ -200,6 +200,9 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
 
     const uint32_t item = blockIdx.x / kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads;
+    // The grid may be sized for more work than this step has (fixed launch
+    // shapes); the step's own count is on the device.
+    if (item >= counts[0]) return;
     const uint32_t row = work[2 * item];
     const uint32_t split = work[2 * item + 1];
     const uint32_t nk = row_num_keys[row];
@@ -391,13 +394,14 @@ template <int HD>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     const uint32_t *__restrict__ row_info, const uint32_t *__restrict__ reduce_rows,
     const float *__restrict__ part_acc, const float *__restrict__ part_ml,
-    uint16_t *__restrict__ out, uint32_t num_heads) {
+    uint16_t *__restrict__ out, uint32_t num_heads, const uint32_t *__restrict__ counts) {
     constexpr int NQ = HD / 4;     // dim quads of one head
     constexpr int P = 256 / NQ;    // split lanes
     __shared__ float s_m[P][NQ];
     __shared__ float s_l[P][NQ];
     __shared__ floatx4 s_acc[P][NQ];
 
+    if (blockIdx.x / num_heads >= counts[1]) return;  // past this step's rows (fixed launch)
     const uint32_t row = reduce_rows[blockIdx.x / num_heads];
     const uint32_t qh = blockIdx.x % num_heads;
     const uint32_t first = row_info[2 * row];
@@ -455,14 +459,14 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                         hipStream_t stream) {
     const uint32_t group = num_heads / pool.kv_heads;
     const size_t smem = (W == 1) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * group * HD) * 4;
-    const uint64_t grid = static_cast<uint64_t>(plan.num_work) * pool.kv_heads;
+    const uint64_t grid = static_cast<uint64_t>(plan.launch_work) * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
     hipLaunchKernelGGL((decode_splitk_kernel<HD, W, NT>), dim3(static_cast<uint32_t>(grid)),
                        dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
                        meta.tables, meta.row_seq, meta.row_num_keys, plan.work, plan.row_info,
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
-                       scale_log2);
+                       scale_log2, plan.counts);
     return hipGetLastError();
 }
 
@@ -482,13 +486,13 @@ hipError_t launch_hd(const PoolLayer &pool, const MetaView &meta, const DecodePl
         default: err = VO_SPLIT(4); break;
     }
 #undef VO_SPLIT
-    if (err != hipSuccess || plan.num_reduce_rows == 0) return err;
-    const uint64_t grid = static_cast<uint64_t>(plan.num_reduce_rows) * num_heads;
+    if (err != hipSuccess || plan.launch_reduce == 0) return err;
+    const uint64_t grid = static_cast<uint64_t>(plan.launch_reduce) * num_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_reduce", stream);
     hipLaunchKernelGGL((decode_reduce_kernel<HD>), dim3(static_cast<uint32_t>(grid)), dim3(256),
                        0, stream, plan.row_info, plan.reduce_rows, plan.part_acc, plan.part_ml,
-                       out, num_heads);
+                       out, num_heads, plan.counts);
     return hipGetLastError();
 }
 
@@ -502,7 +506,7 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               const DecodePlan &plan, const uint16_t *q, uint16_t *out,
                               uint32_t num_heads, float scale, int waves_per_group,
                               hipStream_t stream) {
-    if (plan.num_work == 0) return hipSuccess;
+    if (plan.launch_work == 0) return hipSuccess;
     if (plan.split_keys == 0 || plan.split_keys % kChunk != 0 || plan.split_keys > kMaxSplitKeys)
         return hipErrorInvalidValue;
     const float scale_log2 = scale * 1.4426950408889634f;

@@ -153,6 +153,9 @@ struct DecodePlan {
     float *part_acc;              // [parts][num_heads][head_dim]
     float *part_ml;               // [parts][num_heads][2]: (max, sum), log2 domain
     bool streaming;               // no KV block is read by two rows: non-temporal K/V loads
+    const uint32_t *counts;       // device [2]: num_work, num_reduce_rows; the kernels stop there
+    uint32_t launch_work;         // work items launched (>= num_work; = num_work unless fixed)
+    uint32_t launch_reduce;       // reduce rows launched (>= num_reduce_rows)
 };
 
 // True when the MFMA decode kernel covers this shape.

@@ -90,32 +90,42 @@ extern "C" uint64_t vo_kv_pool_bytes(const vo_kv_pool *pool) { return pool ? poo
 namespace {
 
 // Packs u32 arrays back to back (256-byte aligned) into the staging buffer and
-// records each array's device address.  The buffer is sized at creation for
-// the declared capacities; should a request still not fit, the arrays go to a
-// host-side sink and fits() reports it, so nothing is written out of bounds.
+// records each array's device address.  With fixed launch shapes, each region
+// goes to its fixed offset instead (so its device address is the same in
+// every upload).  The buffer is sized at creation for the declared
+// capacities; should a request still not fit, the arrays go to a host-side
+// sink and fits() reports it, so nothing is written out of bounds.
 class Packer {
    public:
-    explicit Packer(vo_step_meta *m) : m_(m) {}
-    uint32_t *add(uint64_t count, const uint32_t **device_ptr) {
-        off_ = align_up(off_, 256);
-        const uint64_t end = off_ + count * sizeof(uint32_t);
-        if (end > m_->buf_bytes || overflow_) {
-            overflow_ = true;
-            off_ = end;
+    explicit Packer(vo_step_meta *m, bool fixed = false) : m_(m), fixed_(fixed) {
+        if (fixed_) off_ = m_->fixed.bytes;
+    }
+    uint32_t *add(Region region, uint64_t count, const uint32_t **device_ptr) {
+        uint64_t at;
+        if (fixed_) {
+            at = m_->fixed.offset[region];
+            if (count > m_->fixed.cap[region]) overflow_ = true;
+        } else {
+            off_ = align_up(off_, 256);
+            at = off_;
+            off_ = at + count * sizeof(uint32_t);
+            if (off_ > m_->buf_bytes) overflow_ = true;
+        }
+        if (overflow_) {
             sinks_.emplace_back(count + 1);
             *device_ptr = nullptr;
             return sinks_.back().data();
         }
-        uint32_t *host = reinterpret_cast<uint32_t *>(m_->h_stage + off_);
-        *device_ptr = reinterpret_cast<const uint32_t *>(m_->d_buf + off_);
-        off_ = end;
-        return host;
+        *device_ptr = reinterpret_cast<const uint32_t *>(m_->d_buf + at);
+        return reinterpret_cast<uint32_t *>(m_->h_stage + at);
     }
     uint64_t used() const { return off_; }
     bool fits() const { return !overflow_; }
+    bool fixed() const { return fixed_; }
 
    private:
     vo_step_meta *m_;
+    bool fixed_;
     uint64_t off_ = 0;
     bool overflow_ = false;
     std::vector<std::vector<uint32_t>> sinks_;
@@ -210,17 +220,21 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     for (uint32_t s : m->slots) m->max_slot = std::max(m->max_slot, s);
 
     const uint32_t *dp;
-    uint32_t *h = pk.add(num_seqs + 1, &dp);
+    // The split-K counts the kernels read; plan_decode_rows fills them.
+    m->h_counts = pk.add(kRegCounts, 2, &dp);
+    m->h_counts[0] = m->h_counts[1] = 0;
+    m->d_counts = dp;
+    uint32_t *h = pk.add(kRegTableOff, num_seqs + 1, &dp);
     for (uint64_t s = 0; s <= num_seqs; ++s) h[s] = static_cast<uint32_t>(table_off[s]);
     m->view.table_off = dp;
-    h = pk.add(entries, &dp);
+    h = pk.add(kRegTables, entries, &dp);
     if (entries) std::memcpy(h, tables, entries * sizeof(uint32_t));
     m->view.tables = dp;
-    h = pk.add(num_rows, &dp);
+    h = pk.add(kRegRowSeq, num_rows, &dp);
     for (uint64_t r = 0; r < num_rows; ++r)
         h[r] = m->row_seq[r] = row_seq ? static_cast<uint32_t>(row_seq[r]) : 0u;
     m->view.row_seq = dp;
-    h = pk.add(num_rows, &dp);
+    h = pk.add(kRegRowKeys, num_rows, &dp);
     for (uint64_t r = 0; r < num_rows; ++r)
         h[r] = m->row_num_keys[r] = row_num_keys ? static_cast<uint32_t>(row_num_keys[r]) : 0u;
     m->view.row_num_keys = dp;
@@ -231,7 +245,7 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     m->view.positions = nullptr;
     if (positions) {
         m->positions.assign(positions, positions + num_rows);
-        h = pk.add(num_rows, &dp);
+        h = pk.add(kRegPositions, num_rows, &dp);
         for (uint64_t r = 0; r < num_rows; ++r) {
             h[r] = positions[r];
             m->max_position = std::max(m->max_position, positions[r]);
@@ -240,7 +254,7 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     }
     // Write slots: a slot that appears again later keeps only its last row,
     // the reference's "later row wins" copy order (cpu/mod.rs:277-283).
-    h = pk.add(num_rows, &dp);
+    h = pk.add(kRegSlots, num_rows, &dp);
     {
         std::unordered_map<uint32_t, uint64_t> last;
         bool dup = false;
@@ -272,7 +286,7 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
         };
         uint64_t nseg = 0;
         for (uint64_t r = 0; r < num_rows; r = run_end(r)) ++nseg;
-        uint32_t *seg = pk.add(3 * nseg, &dp);
+        uint32_t *seg = pk.add(kRegSegments, 3 * nseg, &dp);
         uint64_t k = 0;
         for (uint64_t r = 0; r < num_rows;) {
             const uint64_t e = run_end(r);
@@ -349,11 +363,11 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     if (parts > m->max_parts) return fail_capacity("split-K partials per step", parts, m->max_parts);
 
     const uint32_t *dp;
-    uint32_t *work = pk.add(2 * parts, &dp);
+    uint32_t *work = pk.add(kRegWork, 2 * parts, &dp);
     m->plan.work = dp;
-    uint32_t *row_info = pk.add(2 * T, &dp);
+    uint32_t *row_info = pk.add(kRegRowInfo, 2 * T, &dp);
     m->plan.row_info = dp;
-    uint32_t *reduce_rows = pk.add(R, &dp);
+    uint32_t *reduce_rows = pk.add(kRegReduceRows, R, &dp);
     m->plan.reduce_rows = dp;
     // Work order, longest first: every full split (L keys) in row order, then
     // each row's shorter last split by descending length.  The hardware deals
@@ -394,9 +408,23 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     m->plan.num_work = static_cast<uint32_t>(parts);
     m->plan.num_reduce_rows = static_cast<uint32_t>(nred);
     m->plan.split_keys = static_cast<uint32_t>(L);
-    m->plan.streaming = decode_streaming(m);
     m->plan.part_acc = m->d_part_acc;
     m->plan.part_ml = m->d_part_ml;
+    m->h_counts[0] = static_cast<uint32_t>(parts);
+    m->h_counts[1] = static_cast<uint32_t>(nred);
+    m->plan.counts = m->d_counts;
+    if (pk.fixed()) {
+        // The same launches every step: capacity-sized grids, the kernels stop
+        // at the counts; the load policy stays the one fixed (it changes no
+        // arithmetic).
+        m->plan.streaming = m->fixed.streaming;
+        m->plan.launch_work = static_cast<uint32_t>(m->fixed.work_cap);
+        m->plan.launch_reduce = static_cast<uint32_t>(m->fixed.seqs);
+    } else {
+        m->plan.streaming = decode_streaming(m);
+        m->plan.launch_work = static_cast<uint32_t>(parts);
+        m->plan.launch_reduce = static_cast<uint32_t>(nred);
+    }
     m->decode_planned = true;
     return VO_OK;
 }
@@ -451,7 +479,7 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
     std::stable_sort(items.begin(), items.end(),
                      [](const Item &a, const Item &b) { return a.tiles > b.tiles; });
     const uint32_t *dp;
-    uint32_t *w = pk.add(4 * items.size(), &dp);
+    uint32_t *w = pk.add(kRegPrefillWork, 4 * items.size(), &dp);
     for (size_t i = 0; i < items.size(); ++i) {
         w[4 * i] = items[i].row;
         w[4 * i + 1] = items[i].rows;
@@ -474,6 +502,38 @@ int decode_waves() {
     return (w == 1 || w == 2 || w == 4 || w == 8) ? w : 4;
 }
 
+
+}  // namespace
+
+namespace {
+
+vo_status refuse_if_fixed(const vo_step_meta *m, const char *op) {
+    if (!m->fixed.on) return VO_OK;
+    return fail_shape(op, "the metadata has fixed launch shapes for decode steps of " +
+                              std::to_string(m->fixed.seqs) +
+                              " sequences; vo_step_meta_unfix_launch first");
+}
+
+// A decode upload fits the fixed launch shapes: same sequence count, table
+// entries and split-K work items within the capacities, positions given iff
+// they were when the shapes were fixed.  Checked before anything changes.
+vo_status check_fixed_decode(const vo_step_meta *m, uint64_t num_seqs, const uint64_t *table_off,
+                             const uint32_t *positions, const uint64_t *row_num_keys) {
+    const FixedLaunch &f = m->fixed;
+    const char *what = "fixed-launch decode step";
+    if (num_seqs != f.seqs || (positions != nullptr) != f.has_positions || !table_off ||
+        (num_seqs && !row_num_keys))
+        return fail_shape("decode", "a fixed-launch decode step takes " + std::to_string(f.seqs) +
+                                        " sequences" +
+                                        (f.has_positions ? " with positions" : " without positions") +
+                                        ", got " + std::to_string(num_seqs));
+    if (table_off[num_seqs] > f.entries_cap) return fail_capacity(what, table_off[num_seqs], f.entries_cap);
+    const uint64_t L = decode_split_keys();
+    uint64_t parts = 0;
+    for (uint64_t r = 0; r < num_seqs; ++r) parts += row_splits(row_num_keys[r], L);
+    if (parts > f.work_cap) return fail_capacity(what, parts, f.work_cap);
+    return VO_OK;
+}
 
 }  // namespace
 
@@ -572,6 +632,7 @@ extern "C" int32_t vo_step_meta_upload_prefill(
     const uint64_t *row_seq, const uint64_t *row_num_keys, void *stream) {
     const char *op = "prefill";
     if (!m) return fail_argument(op, "null meta");
+    if (vo_status rc = refuse_if_fixed(m, op)) return rc;
     if (num_seqs && (!context_lens || !seq_row_starts))
         return fail_argument(op, "null context_lens or seq_row_starts");
     if (seq_row_starts && (seq_row_starts[0] != 0 || seq_row_starts[num_seqs] != num_rows))
@@ -591,7 +652,7 @@ extern "C" int32_t vo_step_meta_upload_prefill(
     {
         // PrefillMeta::last_rows (paged.rs:153-159).
         const uint32_t *dp;
-        uint32_t *h = pk.add(num_seqs, &dp);
+        uint32_t *h = pk.add(kRegLastRows, num_seqs, &dp);
         m->last_rows_ok = true;
         for (uint64_t s = 0; s < num_seqs; ++s) {
             if (seq_row_starts[s + 1] == seq_row_starts[s]) m->last_rows_ok = false;
@@ -616,11 +677,18 @@ extern "C" int32_t vo_step_meta_upload_decode(vo_step_meta *m, uint64_t block_si
                                               const uint64_t *row_num_keys, void *stream) {
     const char *op = "decode";
     if (!m) return fail_argument(op, "null meta");
+    if (m->fixed.on)
+        if (vo_status rc = check_fixed_decode(m, num_seqs, table_off, positions, row_num_keys))
+            return rc;
     DeviceGuard guard(m->device);
-    Packer pk(m);
+    Packer pk(m, m->fixed.on);
     if (vo_status rc = upload_common(m, kDecode, op, block_size, num_seqs, table_off, tables,
                                      num_seqs, slot_mapping, row_seq, row_num_keys, positions, pk))
         return rc;
+    if (m->fixed.on && m->write_plan.num_segments != num_seqs) {
+        m->kind = kNone;
+        return fail_shape(op, "two rows of a fixed-launch decode step share a slot");
+    }
     if (vo_status rc = plan_decode(m, pk)) {
         m->kind = kNone;
         return rc;
@@ -628,7 +696,7 @@ extern "C" int32_t vo_step_meta_upload_decode(vo_step_meta *m, uint64_t block_si
     {
         // Decode: every row is its sequence's last (model.rs:342).
         const uint32_t *dp;
-        uint32_t *h = pk.add(num_seqs, &dp);
+        uint32_t *h = pk.add(kRegLastRows, num_seqs, &dp);
         for (uint64_t s = 0; s < num_seqs; ++s) h[s] = static_cast<uint32_t>(s);
         m->d_last_rows = dp;
         m->last_rows_ok = true;
@@ -646,6 +714,7 @@ extern "C" int32_t vo_step_meta_upload_slots(vo_step_meta *m, const uint32_t *sl
                                              uint64_t num_slots, void *stream) {
     const char *op = "write_kv";
     if (!m) return fail_argument(op, "null meta");
+    if (vo_status rc = refuse_if_fixed(m, op)) return rc;
     DeviceGuard guard(m->device);
     const uint64_t zero = 0;
     Packer pk(m);
@@ -657,6 +726,54 @@ extern "C" int32_t vo_step_meta_upload_slots(vo_step_meta *m, const uint32_t *sl
         return fail_capacity("step metadata bytes", pk.used(), m->buf_bytes);
     }
     if (vo_status rc = finish_upload(m, pk, static_cast<hipStream_t>(stream), op)) return rc;
+    clear_error();
+    return VO_OK;
+}
+
+extern "C" int32_t vo_step_meta_fix_launch(vo_step_meta *m, uint64_t work_headroom,
+                                           uint64_t entry_headroom, void *stream) {
+    const char *op = "fix_launch";
+    if (!m) return fail_argument(op, "null meta");
+    if (m->kind != kDecode || !m->decode_planned)
+        return fail_shape(op, "the last upload must be a decode step");
+    FixedLaunch f;
+    f.on = true;
+    f.seqs = m->num_seqs;
+    f.entries_cap = std::min<uint64_t>(m->tables.size() + entry_headroom, m->max_entries);
+    f.work_cap = std::min<uint64_t>(m->plan.num_work + work_headroom, m->max_parts);
+    f.has_positions = !m->positions.empty() || (m->num_rows == 0 && m->has_positions);
+    f.streaming = m->plan.streaming;
+    const uint64_t S = f.seqs;
+    const uint64_t caps[kNumRegions] = {
+        2, S + 1, f.entries_cap, S, S, f.has_positions ? S : 0, S, 3 * S,
+        2 * f.work_cap, 2 * S, S, S, 0};
+    uint64_t off = 0;
+    for (int r = 0; r < kNumRegions; ++r) {
+        off = align_up(off, 256);
+        f.offset[r] = off;
+        f.cap[r] = caps[r];
+        off += caps[r] * sizeof(uint32_t);
+    }
+    f.bytes = off;
+    if (f.bytes > m->buf_bytes) return fail_capacity("fixed-launch metadata bytes", f.bytes, m->buf_bytes);
+    // Upload the current step again, in the fixed layout.
+    const std::vector<uint64_t> table_off = m->table_off;
+    const std::vector<uint32_t> tables = m->tables, slots = m->slots, positions = m->positions;
+    std::vector<uint64_t> row_seq(m->row_seq.begin(), m->row_seq.end());
+    std::vector<uint64_t> row_keys(m->row_num_keys.begin(), m->row_num_keys.end());
+    const FixedLaunch saved = m->fixed;
+    m->fixed = f;
+    const int32_t rc = vo_step_meta_upload_decode(
+        m, m->block_size, S, table_off.data(), tables.empty() ? nullptr : tables.data(),
+        f.has_positions ? positions.data() : nullptr, slots.data(), row_seq.data(),
+        row_keys.data(), stream);
+    if (rc != VO_OK) m->fixed = saved;
+    return rc;
+}
+
+extern "C" int32_t vo_step_meta_unfix_launch(vo_step_meta *m) {
+    if (!m) return fail_argument("fix_launch", "null meta");
+    m->fixed.on = false;
     clear_error();
     return VO_OK;
 }

@@ -58,6 +58,43 @@ inline vo_status device_status(const char *op, hipError_t err) {
 
 enum MetaKind { kNone = 0, kPrefill = 1, kDecode = 2, kSlots = 3 };
 
+// The arrays of one upload in the metadata buffer.  Ordinary uploads pack
+// them back to back; with fixed launch shapes each has a fixed offset.
+enum Region {
+    kRegCounts = 0,  // [2]: split-K work items, rows to reduce (read by the kernels)
+    kRegTableOff,
+    kRegTables,
+    kRegRowSeq,
+    kRegRowKeys,
+    kRegPositions,
+    kRegSlots,
+    kRegSegments,
+    kRegWork,
+    kRegRowInfo,
+    kRegReduceRows,
+    kRegLastRows,
+    kRegPrefillWork,
+    kNumRegions
+};
+
+// Fixed launch shapes (vo_step_meta_fix_launch): decode uploads of `seqs`
+// sequences put every array at a fixed offset of the metadata buffer, sized
+// by these capacities, and the decode kernels are launched for `work_cap`
+// work items and `seqs` rows to reduce, reading the step's real counts from
+// the device.  Every launch the step makes then has the same arguments and
+// grid from one step to the next, so a HIP graph recorded once replays them.
+struct FixedLaunch {
+    bool on = false;
+    uint64_t seqs = 0;
+    uint64_t entries_cap = 0;
+    uint64_t work_cap = 0;
+    bool has_positions = false;
+    bool streaming = false;
+    uint64_t offset[kNumRegions] = {};  // bytes
+    uint64_t cap[kNumRegions] = {};     // u32 elements
+    uint64_t bytes = 0;
+};
+
 // A row's last, shorter split in the decode work order (keys < split size).
 struct TailItem {
     uint32_t keys, row, split;
@@ -132,6 +169,10 @@ struct vo_step_meta {
     std::vector<uint32_t> decode_rows; // rows of a prefill step planned on the decode kernel
     vo::kernels::PrefillPlan prefill_plan{};
     bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
+
+    vo::FixedLaunch fixed;
+    const uint32_t *d_counts = nullptr;  // [2] device copy of the plan's counts
+    uint32_t *h_counts = nullptr;        // their place in the staging buffer
 
     // Rows the LM head reads (PrefillMeta::last_rows, paged.rs:153-159): each
     // sequence's last row for a prefill upload, every row for a decode upload.

@@ -197,14 +197,18 @@ class Llama:
 
     def enqueue(self, pool: KvPool, tokens, meta, prefill: bool, stream=None) -> None:
         """Everything of one step up to the logits, enqueued without a wait."""
+        m = self.backend._meta_for(pool, meta, stream)
+        m.upload_tokens(tokens, stream)
+        self._launch(pool, m, len(tokens), meta.num_seqs(), prefill, stream)
+
+    def _launch(self, pool: KvPool, m, T: int, S: int, prefill: bool, stream=None) -> None:
+        """The step's device work, from the embedding to the logits, for the
+        metadata and tokens already uploaded into ``m``."""
         c = self.config
         s = _stream_ptr(stream)
-        T, S = len(tokens), meta.num_seqs()
         H, V, hd = c.hidden_size, c.vocab_size, c.head_dim
         qd, kvd, F = self.qd, self.kvd, self.ffn
         eps = float(c.rms_norm_eps)
-        m = self.backend._meta_for(pool, meta, stream)
-        m.upload_tokens(tokens, stream)
         mh = m.handle
         res, nrm, qkv, q, attn = (_ptr(self.residual), _ptr(self.normed), _ptr(self.qkv),
                                   _ptr(self.q), _ptr(self.attn))
@@ -234,6 +238,40 @@ class Llama:
         _check(lib.vo_matmul(g, _ptr(self.last), S, H, _ptr(self.embed), V, H,
                              _ptr(self.logits), f32, 0, s))
 
+    # -- decode steps as a HIP graph ---------------------------------------
+    def capture_decode(self, pool: KvPool, tokens, meta: DecodeMeta, work_headroom=None,
+                       entry_headroom=None) -> "DecodeGraph":
+        """Records the decode step of ``meta``'s sequences (the same count for
+        every later step) as a HIP graph: the metadata is fixed to stable device
+        addresses and capacity-sized launches (vo_step_meta_fix_launch), one
+        eager step builds every GEMM plan, then the device work of a step --
+        embed to argmax into a device buffer -- is recorded.  Replays upload the
+        new step's metadata and tokens, replay, and copy the ids back."""
+        import torch
+        S = meta.num_seqs()
+        self._check_batch(len(tokens), S, S)
+        m = self.backend.step_meta(pool)
+        m.unfix_launch()
+        m.upload(meta)
+        m.fix_launch(S if work_headroom is None else work_headroom,
+                     4 * S + 64 if entry_headroom is None else entry_headroom)
+        m.holds = meta
+        m.upload_tokens(tokens)
+        self._launch(pool, m, S, S, False)
+        self._argmax_device(S)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._launch(pool, m, S, S, False)
+            self._argmax_device(S)
+        return DecodeGraph(self, pool, m, graph, S)
+
+    def _argmax_device(self, S: int, stream=None) -> None:
+        _check(lib.vo_argmax(_ptr(self.logits), VO_DTYPE_F32, S, self.config.vocab_size,
+                             ctypes.cast(ctypes.c_void_p(self.ids.data_ptr()),
+                                         ctypes.POINTER(ctypes.c_uint32)), None,
+                             _stream_ptr(stream)))
+
     def finish(self, num_seqs: int, want_logits: bool, stream=None) -> StepOutput:
         """argmax (the step's one device-to-host wait) and the logits on request."""
         s = _stream_ptr(stream)
@@ -259,3 +297,37 @@ class Llama:
         _check(lib.vo_rope(self.rope.handle, _ptr(self.q), T, qd, hd, m.handle, s))
         _check(lib.vo_rope(self.rope.handle, _ptr(k), T, kvd, hd, m.handle, s))
         _check(lib.vo_write_kv(pool.handle, li, _ptr(k), _ptr(v), T, kvd, m.handle, s))
+
+
+class DecodeGraph:
+    """A recorded decode step (Llama.capture_decode) for a fixed number of
+    sequences.  ``run`` serves any later decode step of those sequences whose
+    metadata fits the fixed capacities; otherwise the upload raises
+    ShapeError / CapacityError and the step must be recorded again."""
+
+    def __init__(self, model: Llama, pool: KvPool, meta_holder, graph, num_seqs: int):
+        self.model, self.pool, self.m, self.graph, self.num_seqs = (model, pool, meta_holder,
+                                                                   graph, num_seqs)
+
+    def run(self, tokens: Sequence[int], meta: DecodeMeta, want_logits: bool = False) -> StepOutput:
+        """Llama::decode (model.rs:234-243) by replaying the recorded launches."""
+        import torch
+        from . import NaNError, VO_ERR_NAN
+        model, S = self.model, self.num_seqs
+        model._check_batch(len(tokens), meta.num_seqs(), meta.num_seqs())
+        if meta.num_seqs() != S:
+            raise _engine_error(ShapeError, VO_ERR_SHAPE, "decode",
+                                f"decode: graph recorded for {S} sequences, step has "
+                                f"{meta.num_seqs()}")
+        if self.m.holds is not meta:
+            self.m.upload(meta)
+            self.m.holds = meta
+        self.m.upload_tokens(tokens)
+        self.graph.replay()
+        model.ids_host[:S].copy_(model.ids[:S])
+        torch.cuda.current_stream().synchronize()
+        ids = model.ids_host[:S].tolist()
+        if any(i == -1 for i in ids):  # 0xffffffff: a row with a NaN
+            raise _engine_error(NaNError, VO_ERR_NAN, "argmax", "argmax: NaN in input")
+        logits = model.logits[:S].cpu().numpy().copy() if want_logits else None
+        return StepOutput([int(i) for i in ids], logits)
