@@ -437,6 +437,13 @@ def bench_model_decode(vo, W, orc, args):
             model.enqueue(wl.pool, tokens, meta, False)
         host = (time.perf_counter() - t0) / 5
         torch.cuda.synchronize()
+        vo.profile_reset()
+        vo.enable_profiling(True)
+        time_steps(torch, step, 5, 0)
+        vo.enable_profiling(False)
+        prof = vo.profile()
+        kernels = {k: round(v["avg_ms"] * v["calls"] / 5, 4)
+                   for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["total_ms"])}
         graph_ms = None
         if args.graph:
             graph = model.capture_decode(wl.pool, tokens, meta)
@@ -456,6 +463,7 @@ def bench_model_decode(vo, W, orc, args):
                                    f"(seed 4), {cfg.num_hidden_layers} layers"},
             "host_enqueue_ms_per_step": round(host * 1e3, 3),
             "graph_ms_per_step": graph_ms,
+            "kernels_ms_per_step": kernels,
             "graph_tokens_per_s": round(S / (graph_ms * 1e-3), 1) if graph_ms else None})
     return lines
 

@@ -715,8 +715,8 @@ class HipBackend:
             per_pool[slot] = m
         return m
 
-    def _meta_for(self, pool: KvPool, meta, stream) -> StepMeta:
-        m = self.step_meta(pool)
+    def _meta_for(self, pool: KvPool, meta, stream, slot: str = "step") -> StepMeta:
+        m = self.step_meta(pool, slot)
         if m.holds is not meta:
             m.upload(meta, stream)
         return m

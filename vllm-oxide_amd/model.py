@@ -126,22 +126,11 @@ class Llama:
             raise ValueError("weights have a different layer count than the config")
         self.rope = RopeTable(hd, c.rope_theta, engine.max_model_len, backend.device,
                               **c.rope_scaling)
-        self.gemm = _vp()
-        _check(lib.vo_gemm_create(backend.device, gemm_workspace, ctypes.byref(self.gemm)))
-
-        T, S, H = engine.max_batch_tokens, engine.max_seqs, c.hidden_size
-        bf, f32 = torch.bfloat16, torch.float32
-        self.residual = torch.empty((T, H), dtype=f32, device=self.dev)
-        self.normed = torch.empty((T, H), dtype=bf, device=self.dev)
-        self.qkv = torch.empty((T, self.qd + 2 * self.kvd), dtype=bf, device=self.dev)
-        self.q = torch.empty((T, self.qd), dtype=bf, device=self.dev)
-        self.attn = torch.empty((T, self.qd), dtype=bf, device=self.dev)
-        self.gu = torch.empty((T, 2 * self.ffn), dtype=bf, device=self.dev)
-        self.act = torch.empty((T, self.ffn), dtype=bf, device=self.dev)
-        self.last = torch.empty((S, H), dtype=bf, device=self.dev)
-        self.logits = torch.empty((S, c.vocab_size), dtype=f32, device=self.dev)
-        self.ids = torch.empty((S,), dtype=torch.int32, device=self.dev)
-        self.ids_host = torch.empty((S,), dtype=torch.int32, pin_memory=True)
+        self._workspace = gemm_workspace
+        self.lanes = [_Lane(self, engine.max_batch_tokens, engine.max_seqs)]
+        lane = self.lanes[0]
+        self.gemm = lane.gemm
+        self.logits, self.ids, self.ids_host = lane.logits, lane.ids, lane.ids_host
 
     def kv_layout(self) -> KvLayout:
         """model.rs:201-212, with the engine's block count."""
@@ -154,9 +143,8 @@ class Llama:
         return self.backend.alloc_kv_pool(self.kv_layout())
 
     def close(self) -> None:
-        if self.gemm:
-            lib.vo_gemm_destroy(self.gemm)
-            self.gemm = _vp()
+        for lane in getattr(self, "lanes", []):
+            lane.close()
 
     def __del__(self):
         try:
@@ -201,19 +189,22 @@ class Llama:
         m.upload_tokens(tokens, stream)
         self._launch(pool, m, len(tokens), meta.num_seqs(), prefill, stream)
 
-    def _launch(self, pool: KvPool, m, T: int, S: int, prefill: bool, stream=None) -> None:
+    def _launch(self, pool: KvPool, m, T: int, S: int, prefill: bool, stream=None,
+                lane=None) -> None:
         """The step's device work, from the embedding to the logits, for the
-        metadata and tokens already uploaded into ``m``."""
+        metadata and tokens already uploaded into ``m``, in ``lane``'s buffers
+        (default: the model's own)."""
         c = self.config
+        B = self.lanes[0] if lane is None else lane
         s = _stream_ptr(stream)
         H, V, hd = c.hidden_size, c.vocab_size, c.head_dim
         qd, kvd, F = self.qd, self.kvd, self.ffn
         eps = float(c.rms_norm_eps)
         mh = m.handle
-        res, nrm, qkv, q, attn = (_ptr(self.residual), _ptr(self.normed), _ptr(self.qkv),
-                                  _ptr(self.q), _ptr(self.attn))
-        gu, act = _ptr(self.gu), _ptr(self.act)
-        g = self.gemm
+        res, nrm, qkv, q, attn = (_ptr(B.residual), _ptr(B.normed), _ptr(B.qkv), _ptr(B.q),
+                                  _ptr(B.attn))
+        gu, act = _ptr(B.gu), _ptr(B.act)
+        g = B.gemm
         bf, f32 = VO_DTYPE_BF16, VO_DTYPE_F32
         fused = pool.layout.block_size == 16 and hd in (64, 128)
         attention = lib.vo_prefill_attention if prefill else lib.vo_decode_attention
@@ -225,18 +216,18 @@ class Llama:
                 _check(lib.vo_qkv_rope_write_kv(pool.handle, li, self.rope.handle, qkv, T, qd,
                                                 kvd, mh, q, s))
             else:
-                self._rope_write_unfused(pool, li, T, m, stream)
+                self._rope_write_unfused(pool, li, T, m, stream, B)
             _check(attention(q, T, qd, pool.handle, li, mh, attn, s))
             _check(lib.vo_matmul(g, attn, T, qd, _ptr(L["wo"]), H, qd, res, f32, 1, s))
             _check(lib.vo_rmsnorm(res, T, H, _ptr(L["mlp_norm"]), H, eps, nrm, s))
             _check(lib.vo_matmul(g, nrm, T, H, _ptr(L["wgu"]), 2 * F, H, gu, bf, 0, s))
-            gu_up = _vp(self.gu.data_ptr() + F * 2)
+            gu_up = _vp(B.gu.data_ptr() + F * 2)
             _check(lib.vo_silu_mul(gu, 2 * F, gu_up, 2 * F, T, F, act, F, s))
             _check(lib.vo_matmul(g, act, T, F, _ptr(L["wd"]), H, F, res, f32, 1, s))
         _check(lib.vo_rmsnorm_last_rows(res, T, H, _ptr(self.final_norm), H, eps, mh,
-                                        _ptr(self.last), s))
-        _check(lib.vo_matmul(g, _ptr(self.last), S, H, _ptr(self.embed), V, H,
-                             _ptr(self.logits), f32, 0, s))
+                                        _ptr(B.last), s))
+        _check(lib.vo_matmul(g, _ptr(B.last), S, H, _ptr(self.embed), V, H,
+                             _ptr(B.logits), f32, 0, s))
 
     # -- decode steps as a HIP graph ---------------------------------------
     def capture_decode(self, pool: KvPool, tokens, meta: DecodeMeta, work_headroom=None,
@@ -285,16 +276,16 @@ class Llama:
         logits = self.logits[:num_seqs].cpu().numpy().copy() if want_logits else None
         return StepOutput(toks, logits)
 
-    def _rope_write_unfused(self, pool: KvPool, li: int, T: int, m, stream) -> None:
+    def _rope_write_unfused(self, pool: KvPool, li: int, T: int, m, stream, L) -> None:
         """Shapes the fused launch does not cover (the reference's tiny test
         model: head_dim 8, block size 4): rope(q), rope(k), write_kv(k, v) as
         three calls on contiguous copies of the q/k/v column blocks."""
         qd, kvd, hd = self.qd, self.kvd, self.config.head_dim
         s = _stream_ptr(stream)
-        self.q[:T].copy_(self.qkv[:T, :qd])
-        k = self.qkv[:T, qd:qd + kvd].contiguous()
-        v = self.qkv[:T, qd + kvd:].contiguous()
-        _check(lib.vo_rope(self.rope.handle, _ptr(self.q), T, qd, hd, m.handle, s))
+        L.q[:T].copy_(L.qkv[:T, :qd])
+        k = L.qkv[:T, qd:qd + kvd].contiguous()
+        v = L.qkv[:T, qd + kvd:].contiguous()
+        _check(lib.vo_rope(self.rope.handle, _ptr(L.q), T, qd, hd, m.handle, s))
         _check(lib.vo_rope(self.rope.handle, _ptr(k), T, kvd, hd, m.handle, s))
         _check(lib.vo_write_kv(pool.handle, li, _ptr(k), _ptr(v), T, kvd, m.handle, s))
 
@@ -331,3 +322,33 @@ class DecodeGraph:
             raise _engine_error(NaNError, VO_ERR_NAN, "argmax", "argmax: NaN in input")
         logits = model.logits[:S].cpu().numpy().copy() if want_logits else None
         return StepOutput([int(i) for i in ids], logits)
+
+
+class _Lane:
+    """Activation buffers and a GEMM handle (with its hipBLASLt workspace) for
+    the steps of one stream, allocated once for max_batch_tokens rows and
+    max_seqs sequences."""
+
+    def __init__(self, model: Llama, T: int, S: int):
+        import torch
+        c, dev = model.config, model.dev
+        H = c.hidden_size
+        bf, f32 = torch.bfloat16, torch.float32
+        self.gemm = _vp()
+        _check(lib.vo_gemm_create(model.backend.device, model._workspace, ctypes.byref(self.gemm)))
+        self.residual = torch.empty((T, H), dtype=f32, device=dev)
+        self.normed = torch.empty((T, H), dtype=bf, device=dev)
+        self.qkv = torch.empty((T, model.qd + 2 * model.kvd), dtype=bf, device=dev)
+        self.q = torch.empty((T, model.qd), dtype=bf, device=dev)
+        self.attn = torch.empty((T, model.qd), dtype=bf, device=dev)
+        self.gu = torch.empty((T, 2 * model.ffn), dtype=bf, device=dev)
+        self.act = torch.empty((T, model.ffn), dtype=bf, device=dev)
+        self.last = torch.empty((S, H), dtype=bf, device=dev)
+        self.logits = torch.empty((S, c.vocab_size), dtype=f32, device=dev)
+        self.ids = torch.empty((S,), dtype=torch.int32, device=dev)
+        self.ids_host = torch.empty((S,), dtype=torch.int32, pin_memory=True)
+
+    def close(self) -> None:
+        if self.gemm:
+            lib.vo_gemm_destroy(self.gemm)
+            self.gemm = _vp()
