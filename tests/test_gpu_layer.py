@@ -77,11 +77,14 @@ def test_matmul_reference_shape_generic_kernel(vo, gpu_backend):
     assert orc.max_rel_diff(_np(got), want) < 1e-6
 
 
-@pytest.mark.parametrize("rows,n,k", [(1, 4096, 4096), (7, 6144, 4096), (300, 1024, 14336),
-                                      (1280, 512, 4096), (4, 1024, 256)])
-def test_matmul_hipblaslt_vs_float64(vo, gpu_backend, rows, n, k):
+@pytest.mark.parametrize("rows,n,k", [(1, 4096, 4096), (3, 1024, 14336), (7, 6144, 4096),
+                                      (16, 1024, 14336), (300, 1024, 14336), (1280, 512, 4096),
+                                      (4, 1024, 256), (17, 512, 4096)])
+def test_matmul_vs_float64(vo, gpu_backend, rows, n, k):
+    """Up to 4 rows run on the weight-streaming kernel (K a multiple of
+    2048), the rest on hipBLASLt."""
     import torch
-    _say(f"matmul hipblaslt {rows}x{k} . {n}x{k}^T")
+    _say(f"matmul {rows}x{k} . {n}x{k}^T")
     rng = np.random.default_rng(rows + n + k)
     x = W.round_bf16(rng.standard_normal((rows, k), np.float32))
     w = W.round_bf16(rng.standard_normal((n, k), np.float32) * np.float32(0.02))
@@ -102,6 +105,24 @@ def test_matmul_hipblaslt_vs_float64(vo, gpu_backend, rows, n, k):
     acc = _dev(base, torch.float32)
     gpu_backend.matmul(xd, wd, out=acc, accumulate=True)
     assert orc.max_rel_diff(_np(acc), base.astype(np.float64) + want) < 1e-5
+
+
+def test_skinny_matmul_rows_independent_of_batch(vo, gpu_backend):
+    """The weight-streaming kernel's output for a row does not depend on the
+    other rows of the batch: each of 4 rows equals, bitwise, the same row
+    computed alone (and the 3-row prefix equals the 4-row call's)."""
+    import torch
+    _say("skinny matmul batch independence")
+    rng = np.random.default_rng(9)
+    x = W.round_bf16(rng.standard_normal((4, 4096), np.float32))
+    w = W.round_bf16(rng.standard_normal((6144, 4096), np.float32) * np.float32(0.02))
+    xd, wd = _dev(x, torch.bfloat16), _dev(w, torch.bfloat16)
+    full = _np(gpu_backend.matmul(xd, wd, out_dtype=torch.float32))
+    for r in (0, 1, 3):
+        one = _np(gpu_backend.matmul(xd[r:r + 1].contiguous(), wd, out_dtype=torch.float32))
+        assert np.array_equal(one[0], full[r]), r
+    part = _np(gpu_backend.matmul(xd[:3].contiguous(), wd, out_dtype=torch.float32))
+    assert np.array_equal(part, full[:3])
 
 
 def test_matmul_rejects_mismatched_shapes(vo, gpu_backend):

@@ -279,6 +279,72 @@ __global__ __launch_bounds__(kThreads) void matmul_generic_kernel(
     }
 }
 
+// Backend::matmul for 1..4 rows (small decode batches): streaming the
+// weight is the whole cost.  A workgroup owns 16 weight rows (outputs) and
+// splits K over its 8 wavefronts; each wavefront runs
+// v_mfma_f32_16x16x32_bf16 with A = 16 weight rows x 32 k (one non-temporal
+// 16-byte load per lane) and B = x^T (the batch rows in columns 0..rows-1;
+// columns past the batch repeat its last row and are not stored, so no lane
+// branches), 8 steps of loads issued before their MFMAs.  The 8 partial
+// tiles are summed through LDS in wavefront order, so an output depends
+// only on its own row of x, whatever the batch size.  Beyond 4 rows the
+// repeated x reads (every workgroup reads all of x) make hipBLASLt faster.
+// MODE 0: bf16 out, 1: f32 out, 2: f32 out += .
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyU = 8;     // 32-k steps per load batch
+constexpr int kSkinnyRows = 4;  // largest batch the kernel is used for
+
+template <int MODE>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void skinny_gemm_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ w, uint32_t rows, uint32_t n,
+    uint32_t k, void *__restrict__ out) {
+    constexpr int U = kSkinnyU;
+    __shared__ floatx4 part[kSkinnyWaves][64];
+    const uint32_t n0 = blockIdx.x * 16;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t kw = k / kSkinnyWaves;  // a multiple of 32 * U
+    const uint32_t r = lane & 15, kg = lane >> 4;
+    const uint16_t *wp = w + static_cast<uint64_t>(n0 + r) * k + wave * kw + 8 * kg;
+    const bool live = r < rows;
+    const uint16_t *xp = x + static_cast<uint64_t>(min(r, rows - 1)) * k + wave * kw + 8 * kg;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t kk = 0; kk < kw; kk += 32 * U) {
+        u32x4 a[U], b[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            a[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wp + kk + 32 * u));
+            b[u] = *reinterpret_cast<const u32x4 *>(xp + kk + 32 * u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[u]),
+                                                          __builtin_bit_cast(bf16x8, b[u]), acc,
+                                                          0, 0, 0);
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    floatx4 t = part[0][lane];
+#pragma unroll
+    for (int v = 1; v < kSkinnyWaves; ++v) t += part[v][lane];
+    // Lane l holds outputs n0 + 4 (l / 16) + e, e = 0..3, of batch row l % 16.
+    if (!live) return;
+    const uint64_t o = static_cast<uint64_t>(r) * n + n0 + 4 * kg;
+    if constexpr (MODE == 0) {
+        u32x2 p;
+        p[0] = static_cast<uint32_t>(f32_to_bf16_bits(t[0])) |
+               (static_cast<uint32_t>(f32_to_bf16_bits(t[1])) << 16);
+        p[1] = static_cast<uint32_t>(f32_to_bf16_bits(t[2])) |
+               (static_cast<uint32_t>(f32_to_bf16_bits(t[3])) << 16);
+        *reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(out) + o) = p;
+    } else {
+        floatx4 *d = reinterpret_cast<floatx4 *>(static_cast<float *>(out) + o);
+        if constexpr (MODE == 2) t += *d;
+        *d = t;
+    }
+}
+
 uint32_t grid_for(uint64_t items) {
     const uint64_t g = (items + kThreads - 1) / kThreads;
     return static_cast<uint32_t>(g < 65536 ? (g ? g : 1) : 65536);
@@ -377,6 +443,32 @@ hipError_t launch_matmul_generic(const uint16_t *x, const uint16_t *w, uint32_t 
     else
         hipLaunchKernelGGL((matmul_generic_kernel<false>), dim3(static_cast<uint32_t>(grid)),
                            dim3(kThreads), 0, stream, x, w, rows, n, k, out, accumulate);
+    return hipGetLastError();
+}
+
+}  // namespace kernels
+}  // namespace vo
+
+namespace vo {
+namespace kernels {
+
+bool skinny_gemm_supported(uint64_t rows, uint64_t n, uint64_t k) {
+    return rows >= 1 && rows <= kSkinnyRows && n % 16 == 0 &&
+           k % (kSkinnyWaves * 32 * kSkinnyU) == 0 && n / 16 <= 0x7fffffffull;
+}
+
+hipError_t launch_skinny_gemm(const uint16_t *x, const uint16_t *w, uint32_t rows, uint32_t n,
+                              uint32_t k, void *out, bool out_f32, bool accumulate,
+                              hipStream_t stream) {
+    if (!skinny_gemm_supported(rows, n, k)) return hipErrorInvalidValue;
+    KernelTimer timer("matmul_skinny", stream);
+    const dim3 grid(n / 16), block(64 * kSkinnyWaves);
+    if (!out_f32)
+        hipLaunchKernelGGL((skinny_gemm_kernel<0>), grid, block, 0, stream, x, w, rows, n, k, out);
+    else if (!accumulate)
+        hipLaunchKernelGGL((skinny_gemm_kernel<1>), grid, block, 0, stream, x, w, rows, n, k, out);
+    else
+        hipLaunchKernelGGL((skinny_gemm_kernel<2>), grid, block, 0, stream, x, w, rows, n, k, out);
     return hipGetLastError();
 }
 

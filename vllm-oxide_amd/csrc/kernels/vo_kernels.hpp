@@ -134,6 +134,12 @@ hipError_t launch_silu_mul(const uint16_t *gate, uint32_t gate_ld, const uint16_
                            uint32_t out_ld, bool vec8, hipStream_t stream);
 hipError_t launch_argmax(const void *logits, bool f32, uint32_t rows, uint32_t cols, uint32_t *ids,
                          hipStream_t stream);
+// Weight-streaming GEMM for 1..4 rows (small decode batches): n % 16 == 0,
+// k % 2048 == 0.
+bool skinny_gemm_supported(uint64_t rows, uint64_t n, uint64_t k);
+hipError_t launch_skinny_gemm(const uint16_t *x, const uint16_t *w, uint32_t rows, uint32_t n,
+                              uint32_t k, void *out, bool out_f32, bool accumulate,
+                              hipStream_t stream);
 hipError_t launch_matmul_generic(const uint16_t *x, const uint16_t *w, uint32_t rows, uint32_t n,
                                  uint32_t k, void *out, bool out_f32, bool accumulate,
                                  hipStream_t stream);

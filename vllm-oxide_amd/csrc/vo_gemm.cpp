@@ -306,6 +306,16 @@ extern "C" int32_t vo_matmul(vo_gemm *g, const void *x, uint64_t rows, uint64_t 
                                      static_cast<uint32_t>(in_features), out,
                                      out_dtype == VO_DTYPE_F32, accumulate != 0,
                                      static_cast<hipStream_t>(stream)));
+    // Decode-sized batches: the weight-streaming kernel (VO_SKINNY_GEMM=0: off).
+    static const bool skinny_on = env_int("VO_SKINNY_GEMM", 1) != 0;
+    if (skinny_on && kernels::skinny_gemm_supported(rows, out_features, in_features))
+        return device_status(op, kernels::launch_skinny_gemm(
+                                     static_cast<const uint16_t *>(x),
+                                     static_cast<const uint16_t *>(weight),
+                                     static_cast<uint32_t>(rows), static_cast<uint32_t>(out_features),
+                                     static_cast<uint32_t>(in_features), out,
+                                     out_dtype == VO_DTYPE_F32, accumulate != 0,
+                                     static_cast<hipStream_t>(stream)));
     const LtApi &api = lt_api();
     Plan *plan;
     {
