@@ -199,17 +199,100 @@ def cpu_baseline(orc, W, wl, nbytes, args):
         if time.perf_counter() >= t_end or len(times) >= 2000:
             break
     med = float(np.median(times))
+    t0 = time.perf_counter()
+    W.oracle_attention(orc, wl, pool=pool, threads=1)
+    single = time.perf_counter() - t0
     S = wl.rows
     return {
         "value": round(nbytes / med / 1e9, 2),
         "unit": "GB/s",
         "tokens_per_s": round(S / med, 2),
         "ms_per_step": round(med * 1e3, 2),
+        "single_thread_ms_per_step": round(single * 1e3, 2),
         "cores": threads,
         "kind": "port",
         "cpu": model,
         "sample": (f"full decode_attention of the same step ({S} rows, f32 oracle on the bf16 "
                    f"inputs), median of {len(times)} runs; same algorithmic-byte definition"),
+    }
+
+
+def cpu_baseline_model(orc, W, cfg, ctx, new, args):
+    """The oracle's Llama layer (model.rs:269-356 restated in C) on a bounded
+    sample of the cfg4 step: one decoder layer for 32 of its 1280 rows -- 8
+    decode rows (the step's first 8 sequences, their cached contexts) and 24
+    rows of a prefill chunk (positions 2024..2047 of the chunk whose context
+    is 1536) -- with f32 weights ~ N(0, 0.02), plus the LM head for 8 rows.
+    Scaled linearly to the step: 32 layers x 1280 rows and 258 LM-head rows
+    (the GEMMs, 94% of the reference's CPU time, scale with rows)."""
+    model_name, avail = cpu_info()
+    threads = min(avail, args.cpu_threads)
+    rng = np.random.default_rng(14)
+    H, F, V, hd = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.head_dim
+    KVH, NH = cfg.num_key_value_heads, cfg.num_attention_heads
+    qd, kvd = NH * hd, KVH * hd
+
+    def nrm(o, i):
+        return (rng.standard_normal((o, i), np.float32) * np.float32(0.02)).astype(np.float32)
+
+    L = dict(wq=nrm(qd, H), wk=nrm(kvd, H), wv=nrm(kvd, H), wo=nrm(H, qd), w_gate=nrm(F, H),
+             w_up=nrm(F, H), w_down=nrm(H, F), norm=np.ones(H, np.float32))
+    embed = nrm(V, H)
+    dec = [int(c) for c in ctx[:8]]
+    chunk_ctx, chunk_rows = 1536 + 512 - 24, 24
+    seqs = [(c, 1) for c in dec] + [(chunk_ctx, chunk_rows)]
+    bs = 16
+    nblk = [-(-(c + n) // bs) for c, n in seqs]
+    perm = rng.permutation(sum(nblk)).astype(np.uint32)
+    tables, at = [], 0
+    for b in nblk:
+        tables.append(perm[at:at + b])
+        at += b
+    pool = orc.Pool(1, sum(nblk), bs, KVH, hd)
+    for (c, _), t in zip(seqs, tables):
+        if c:
+            slots = [int(t[p // bs]) * bs + p % bs for p in range(c)]
+            pool.write_kv(0, rng.standard_normal((c, kvd), np.float32),
+                          rng.standard_normal((c, kvd), np.float32), slots)
+    meta = orc.prefill_meta([(c, n, t) for (c, n), t in zip(seqs, tables)], bs)
+    inv = orc.rope_inv_freq(hd, cfg.rope_theta, **cfg.rope_scaling)
+    cos, sin = orc.rope_table(inv, 8192 + 1024)
+    rows = len(meta["positions"])
+    x = rng.standard_normal((rows, H), np.float32)
+    eps = np.float32(cfg.rms_norm_eps)
+
+    def layer():
+        n = orc.rmsnorm(x, L["norm"], eps)
+        q = orc.rope_apply(orc.matmul(n, L["wq"], threads), meta["positions"], cos, sin)
+        k = orc.rope_apply(orc.matmul(n, L["wk"], threads), meta["positions"], cos, sin)
+        v = orc.matmul(n, L["wv"], threads)
+        pool.write_kv(0, k, v, meta["slot_mapping"])
+        a = pool.attention(q, 0, tables, meta["row_seq"], meta["row_num_keys"], threads)
+        h = orc.add(x, orc.matmul(a, L["wo"], threads))
+        n = orc.rmsnorm(h, L["norm"], eps)
+        act = orc.silu_mul(orc.matmul(n, L["w_gate"], threads), orc.matmul(n, L["w_up"], threads))
+        return orc.add(h, orc.matmul(act, L["w_down"], threads))
+
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    while True:
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= 50:
+            break
+    t_layer = float(np.median(times))
+    t0 = time.perf_counter()
+    orc.argmax(orc.matmul(orc.rmsnorm(x[:8], L["norm"], eps), embed, threads))
+    t_head = time.perf_counter() - t0
+    step = cfg.num_hidden_layers * t_layer * (1280 / rows) + t_head * (258 / 8)
+    return {
+        "value": round(1280 / step, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "cpu": model_name, "est_ms_per_step": round(step * 1e3, 1),
+        "sample": (f"one decoder layer for {rows} of the step's 1280 rows (8 decode rows with "
+                   f"their contexts, 24 rows of the 1536-context chunk) and the LM head for 8 "
+                   f"rows, f32 oracle, median of {len(times)} layer runs; scaled to 32 layers x "
+                   f"1280 rows + 258 LM-head rows"),
     }
 
 
@@ -376,7 +459,7 @@ def bench_model(vo, W, orc, args):
         "kernels_ms_per_step": {k: round(v["avg_ms"] * v["calls"] / prof_steps, 4)
                                 for k, v in sorted(prof.items(),
                                                    key=lambda kv: -kv[1]["avg_ms"] * kv[1]["calls"])},
-        "cpu_baseline": None,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_model(orc, W, cfg, ctx, new, args),
     }
 
 
