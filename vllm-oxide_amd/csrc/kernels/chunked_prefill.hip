@@ -347,7 +347,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ---------------------------------------------------------------------------
 // The same kernel with the KV tiles staged by LDS DMA (gfx950
-// global_load_lds_dwordx4: each lane's 16 bytes go from its own global
+// buffer_load_dwordx4 ... lds: each lane's 16 bytes go from its own global
 // address straight into LDS at base + 16 * lane) through a ring of three LDS
 // stages, so the tile two ahead is in flight while this one is computed and
 // no registers or ds_write instructions carry the staging.
@@ -384,6 +384,26 @@ struct DmaShape {
     static constexpr int DPW = 2 * NK / W;        // per wave: DPW/2 for K, DPW/2 for V
     static_assert((2 * NK) % W == 0 && DPW % 2 == 0 && DPW <= 15, "DMA split");
 };
+
+// Word 3 of a raw buffer resource on gfx950 (32-bit data format, no swizzle).
+constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;
+
+// LDS DMA of 16 bytes per lane: bytes [voff, voff + 16) of the buffer at base
+// (wave-uniform, `bytes` long) to lds + 16 * lane.  The MUBUF form is used
+// rather than global_load_lds: the compiler counts a pending FLAT-encoded LDS
+// DMA against the LDS counter too and then waits for every outstanding LDS
+// read (lgkmcnt(0)) wherever it needs one, while a MUBUF DMA counts only in
+// vmcnt and the ds_read waits stay partial.
+__device__ __forceinline__ void dma16(const void *base, uint32_t bytes, void *lds, uint32_t voff) {
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufferRsrcWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds,
+                                             16, voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t x) {
+    return __builtin_amdgcn_readfirstlane(x);
+}
 
 // s_waitcnt vmcnt(N) lgkmcnt(0), then a workgroup barrier.
 template <int N>
@@ -470,7 +490,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2)))
         const uint32_t qi = (i % (DPW / 2)) * W + wave;
         const uint32_t P = 64 * (qi % D::IPB) + lane;
         const uint32_t U = i < DPW / 2 ? P ^ ((P >> 4) & 3u) : P ^ ((P >> 4) & 1u);
-        dma_off[i] = U * 8;
+        dma_off[i] = U * 16;
     }
     auto dma_tile = [&](uint8_t *stage, uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
 #pragma unroll
@@ -479,12 +499,13 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2)))
             const uint32_t qi = (i % (DPW / 2)) * W + wave;
             const uint32_t blk = pick4(b0, b1, b2, b3, qi / D::IPB);
             const uint16_t *pool = is_k ? k_pool : v_pool;
-            const uint16_t *src = pool + (static_cast<uint64_t>(blk) * kv_heads + kvh) * kTile + dma_off[i];
-            uint8_t *dst = stage + (is_k ? 0 : D::KBYTES) + qi * 1024;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            const uint16_t *tile_src = pool + (static_cast<uint64_t>(blk) * kv_heads + kvh) * kTile;
+            dma16(tile_src, D::BT, stage + (is_k ? 0 : D::KBYTES) + qi * 1024, dma_off[i]);
         }
     };
-    auto blk_of = [&](uint32_t t, int b) { return tbl[min(4 * t + b, nblk - 1)]; };
+    auto blk_of = [&](uint32_t t, int b) {
+        return uniform_u32(tbl[min(4 * t + b, nblk - 1)]);
+    };
 
     float m_run = 0.0f;
     float l_run = 0.0f;
