@@ -62,11 +62,10 @@ def cpu_info():
     return model, avail
 
 
-def traffic_record(kernel, workload):
-    """Counter-measured HBM bytes per launch, from the committed rocprofv3
-    --pmc summary for this kernel and workload (profiles/*.json), or None.
-    A record counts only while the kernel source it was measured on is
-    unchanged (sha256 prefix of the source file)."""
+def profile_record(kernel, workload):
+    """The committed rocprofv3 --pmc record (profiles/*.json) for this kernel
+    and workload, or None.  A record counts only while the kernel source it
+    was measured on is unchanged (sha256 prefix of the source file)."""
     import hashlib
     for p in sorted((ROOT / "profiles").glob("*.json")):
         try:
@@ -80,8 +79,15 @@ def traffic_record(kernel, workload):
             continue
         if hashlib.sha256(src.read_bytes()).hexdigest()[:16] != rec.get("source_sha256_16"):
             continue
-        return rec.get("hbm_bytes_per_launch")
+        return rec
     return None
+
+
+def traffic_record(kernel, workload):
+    """Counter-measured HBM bytes per launch (FETCH_SIZE and WRITE_SIZE,
+    scaled by a device copy's readings), or None."""
+    rec = profile_record(kernel, workload)
+    return rec.get("hbm_bytes_per_launch") if rec else None
 
 
 def time_steps(torch, fn, steps, warmup):
@@ -320,18 +326,22 @@ def bench_prefill(vo, W, orc, args):
     flops = wl.attention_flops()
     kern = max(prof.items(), key=lambda kv: kv[1]["total_ms"])
     k_s = kern[1]["avg_ms"] / 1e3
+    workload = "cfg3: 8 seqs x 512-row chunk, ctx U[0,8192] seed 3"
+    rec = profile_record(kern[0], workload) or {}
     return {
         "metric": "chunked prefill attention TFLOP/s (causal-aware), Llama-3-8B shape, 1 GPU",
         "value": round(flops / sec / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "cfg3: 8 seqs x 512-row chunk, ctx U[0,8192] seed 3",
-                   "step": "write_kv + prefill_attention"},
+        "config": {"workload": workload, "step": "write_kv + prefill_attention"},
         "kernels_us": {k: round(v["avg_ms"] * 1e3, 2) for k, v in prof.items()},
         "roofline": {"bound": "mfma", "kernel": kern[0],
                      "achieved": round(flops / k_s / 1e12, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(flops / k_s / 1e12 / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": rec.get("hbm_bytes_per_launch"),
+                     # Cycles the MFMA pipe was busy / all cycles, from the
+                     # committed counter record (SQ_VALU_MFMA_BUSY_CYCLES).
+                     "mfma_busy": rec.get("mfma_busy_frac")},
     }
 
 
