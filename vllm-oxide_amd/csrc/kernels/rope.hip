@@ -154,6 +154,9 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
 
 #pragma unroll
     for (uint32_t j = 0; j < KI; ++j) {
+        // Passes wholly past the run are skipped (n is the same for the whole
+        // wavefront); a one-row run of a decode step takes one pass.
+        if (RPI * j >= n) break;
         const uint32_t i = i0 + RPI * j;
         // Every lane of a row takes part in the shuffles, so rows past the
         // run clamp to its last row and skip only the stores.
@@ -170,12 +173,23 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
         const u32x4 kout = rot(kin, c, s);
         if (live && cache)
             *reinterpret_cast<u32x4 *>(k_pool + tile + (d / 32) * (BS * 32) + (off0 + i) * 32 + d % 32) = kout;
-        for (uint32_t h = 0; h < group; ++h) {
-            const uint32_t col = (kvh * group + h) * HD + d;
-            const u32x4 qin =
-                *reinterpret_cast<const u32x4 *>(q_in + static_cast<uint64_t>(row) * q_in_ld + col);
-            const u32x4 qout = rot(qin, c, s);
-            if (live) *reinterpret_cast<u32x4 *>(q_out + static_cast<uint64_t>(row) * q_out_ld + col) = qout;
+        // The G query heads four at a time, loads first, so that four loads
+        // are in flight rather than one.
+        for (uint32_t h0 = 0; h0 < group; h0 += 4) {
+            u32x4 qin[4];
+#pragma unroll
+            for (uint32_t hh = 0; hh < 4; ++hh) {
+                const uint32_t h = min(h0 + hh, group - 1);
+                const uint32_t col = (kvh * group + h) * HD + d;
+                qin[hh] = *reinterpret_cast<const u32x4 *>(q_in + static_cast<uint64_t>(row) * q_in_ld + col);
+            }
+#pragma unroll
+            for (uint32_t hh = 0; hh < 4; ++hh) {
+                const uint32_t col = (kvh * group + h0 + hh) * HD + d;
+                const u32x4 qout = rot(qin[hh], c, s);
+                if (live && h0 + hh < group)
+                    *reinterpret_cast<u32x4 *>(q_out + static_cast<uint64_t>(row) * q_out_ld + col) = qout;
+            }
         }
     }
 
