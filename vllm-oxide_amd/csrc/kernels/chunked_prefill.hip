@@ -669,20 +669,28 @@ bool prefill_use_dma() {
     return dma;
 }
 
-template <int HD, int G>
-hipError_t launch_g(const PoolLayer &pool, const MetaView &meta, const PrefillPlan &plan,
-                    const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
-                    hipStream_t stream) {
-    // Eight waves per workgroup: two row groups for up to 4 heads, one for 8.
-    constexpr int R = G <= 4 ? 2 : 1;
+// VO_PREFILL_NARROW=0 keeps 64-row workgroups on small grids (A/B).
+bool prefill_narrow_enabled() {
+    static const bool on = [] {
+        const char *v = std::getenv("VO_PREFILL_NARROW");
+        return !(v && std::string(v) == "0");
+    }();
+    return on;
+}
+
+template <int HD, int G, int R>
+hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillPlan &plan,
+                     const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
+                     hipStream_t stream) {
     constexpr int HALVES = kQT / (kRG * R);
     const uint64_t grid = static_cast<uint64_t>(plan.num_items) * HALVES * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("prefill_mfma", stream);
     // The DMA kernel stages a sequence's whole block table in LDS, and its
     // three 32 KiB stages at head_dim 128 leave room for one workgroup per
-    // CU, which takes 8 wavefronts to fill the SIMDs.
-    constexpr bool dma_shape = HD == 64 || G * R == 8;
+    // CU, which takes 8 wavefronts to fill the SIMDs -- or 4 when the grid
+    // has fewer workgroups than CUs anyway (32-row workgroups below).
+    constexpr bool dma_shape = HD == 64 || G * R == 8 || (G == 4 && R == 1);
     if constexpr (dma_shape) {
         if (prefill_use_dma() && plan.max_keys <= kTableLds * kBS) {
             hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
@@ -698,14 +706,32 @@ hipError_t launch_g(const PoolLayer &pool, const MetaView &meta, const PrefillPl
     return hipGetLastError();
 }
 
+template <int HD, int G>
+hipError_t launch_g(const PoolLayer &pool, const MetaView &meta, const PrefillPlan &plan,
+                    const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
+                    uint32_t num_cus, hipStream_t stream) {
+    // Eight waves per workgroup: two row groups for up to 4 heads, one for 8.
+    // A grid of fewer 64-row workgroups than CUs (a few long chunks, as in a
+    // mixed serving step) leaves CUs idle while its longest items run; 32-row
+    // workgroups of 4 wavefronts then double the grid and halve each
+    // workgroup's MFMA work per KV tile.
+    if constexpr (G == 4) {
+        if (prefill_narrow_enabled() &&
+            static_cast<uint64_t>(plan.num_items) * pool.kv_heads < num_cus)
+            return launch_gr<HD, 4, 1>(pool, meta, plan, q, out, num_heads, scale_log2, stream);
+    }
+    return launch_gr<HD, G, (G <= 4 ? 2 : 1)>(pool, meta, plan, q, out, num_heads, scale_log2,
+                                              stream);
+}
+
 template <int HD>
 hipError_t launch_hd(const PoolLayer &pool, const MetaView &meta, const PrefillPlan &plan,
                      const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
-                     hipStream_t stream) {
+                     uint32_t num_cus, hipStream_t stream) {
     switch (num_heads / pool.kv_heads) {
-        case 2: return launch_g<HD, 2>(pool, meta, plan, q, out, num_heads, scale_log2, stream);
-        case 4: return launch_g<HD, 4>(pool, meta, plan, q, out, num_heads, scale_log2, stream);
-        case 8: return launch_g<HD, 8>(pool, meta, plan, q, out, num_heads, scale_log2, stream);
+        case 2: return launch_g<HD, 2>(pool, meta, plan, q, out, num_heads, scale_log2, num_cus, stream);
+        case 4: return launch_g<HD, 4>(pool, meta, plan, q, out, num_heads, scale_log2, num_cus, stream);
+        case 8: return launch_g<HD, 8>(pool, meta, plan, q, out, num_heads, scale_log2, num_cus, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -721,12 +747,13 @@ uint32_t prefill_rows_per_tile() { return kQT; }
 
 hipError_t launch_prefill_mfma(const PoolLayer &pool, const MetaView &meta,
                                const PrefillPlan &plan, const uint16_t *q, uint16_t *out,
-                               uint32_t num_heads, float scale, hipStream_t stream) {
+                               uint32_t num_heads, float scale, uint32_t num_cus,
+                               hipStream_t stream) {
     if (plan.num_items == 0) return hipSuccess;
     const float scale_log2 = scale * 1.4426950408889634f;
     switch (pool.head_dim) {
-        case 64: return launch_hd<64>(pool, meta, plan, q, out, num_heads, scale_log2, stream);
-        case 128: return launch_hd<128>(pool, meta, plan, q, out, num_heads, scale_log2, stream);
+        case 64: return launch_hd<64>(pool, meta, plan, q, out, num_heads, scale_log2, num_cus, stream);
+        case 128: return launch_hd<128>(pool, meta, plan, q, out, num_heads, scale_log2, num_cus, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -187,9 +187,12 @@ bool prefill_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t gro
 // Query rows per work item of the MFMA prefill kernel.
 uint32_t prefill_rows_per_tile();
 
+// num_cus: compute units of the device (0 if unknown); a plan with fewer
+// 64-row workgroups than CUs runs on 32-row workgroups.
 hipError_t launch_prefill_mfma(const PoolLayer &pool, const MetaView &meta,
                                const PrefillPlan &plan, const uint16_t *q, uint16_t *out,
-                               uint32_t num_heads, float scale, hipStream_t stream);
+                               uint32_t num_heads, float scale, uint32_t num_cus,
+                               hipStream_t stream);
 
 }  // namespace kernels
 }  // namespace vo

@@ -1148,7 +1148,8 @@ extern "C" int32_t vo_prefill_attention(const void *queries, uint64_t rows, uint
         const hipStream_t st = static_cast<hipStream_t>(stream);
         err = kernels::launch_prefill_mfma(pool->layer(layer), m->view, m->prefill_plan,
                                            static_cast<const uint16_t *>(queries),
-                                           static_cast<uint16_t *>(out), heads, scale, st);
+                                           static_cast<uint16_t *>(out), heads, scale,
+                                           pool->num_cus, st);
         // Sequences with one new row (the decode rows of a mixed step).
         if (err == hipSuccess && m->decode_planned)
             err = kernels::launch_decode_mfma(pool->layer(layer), m->view, m->plan,
