@@ -419,8 +419,12 @@ __device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t c, ui
     return i < 2 ? (i == 0 ? a : b) : (i == 2 ? c : d);
 }
 
+// Occupancy target: two wavefronts per SIMD, except at head_dim 128 with 4
+// wavefronts per workgroup, where the 112 KiB of LDS leaves one workgroup per
+// CU and so one wavefront per SIMD.
 template <int HD, int G, int R>
-__global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(2))) void prefill_dma_kernel(
+__global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
+    (HD == 128 && G * R == 4) ? 1 : 2))) void prefill_dma_kernel(
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
     const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
     const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
