@@ -497,6 +497,13 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
     return VO_OK;
 }
 
+// VO_MIXED_OVERLAP=0 runs a mixed step's decode rows after its chunks on the
+// caller's stream (A/B).
+bool mixed_overlap_enabled() {
+    static const bool on = env_int("VO_MIXED_OVERLAP", 1) != 0;
+    return on;
+}
+
 int decode_waves() {
     int w = env_int("VO_DECODE_WAVES", 4);
     return (w == 1 || w == 2 || w == 4 || w == 8) ? w : 4;
@@ -591,6 +598,10 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
         err = hipHostMalloc(reinterpret_cast<void **>(&m->h_tokens), max_rows * sizeof(uint32_t),
                             hipHostMallocDefault);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&m->tokens_done, hipEventDisableTiming);
+    // Default priority, like every stream here.
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&m->fork, hipEventDisableTiming);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&m->join, hipEventDisableTiming);
     if (err != hipSuccess) {
         vo_status rc = fail_device(op, err, hipGetErrorString(err));
         if (m->d_tokens) (void)hipFree(m->d_tokens);
@@ -601,6 +612,9 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
         if (m->d_part_acc) (void)hipFree(m->d_part_acc);
         if (m->d_part_ml) (void)hipFree(m->d_part_ml);
         if (m->copy_done) (void)hipEventDestroy(m->copy_done);
+        if (m->side) (void)hipStreamDestroy(m->side);
+        if (m->fork) (void)hipEventDestroy(m->fork);
+        if (m->join) (void)hipEventDestroy(m->join);
         delete m;
         return rc;
     }
@@ -622,6 +636,12 @@ extern "C" void vo_step_meta_destroy(vo_step_meta *m) {
     (void)hipHostFree(m->h_stage);
     (void)hipFree(m->d_part_acc);
     (void)hipFree(m->d_part_ml);
+    if (m->side) {
+        (void)hipStreamSynchronize(m->side);
+        (void)hipStreamDestroy(m->side);
+    }
+    if (m->fork) (void)hipEventDestroy(m->fork);
+    if (m->join) (void)hipEventDestroy(m->join);
     delete m;
 }
 
@@ -1141,21 +1161,35 @@ extern "C" int32_t vo_prefill_attention(const void *queries, uint64_t rows, uint
     if (m->prefill_planned &&
         kernels::prefill_mfma_supported(static_cast<uint32_t>(L.head_dim),
                                         static_cast<uint32_t>(L.block_size), group)) {
-        // A mixed step's chunks and decode rows write disjoint rows of `out`.
-        // (Running the two launches concurrently on two streams measured no
-        // faster: the decode workgroups take the CUs the long prefill
-        // workgroups need, and the chunks then finish last.)
+        // A mixed step's chunks and decode rows write disjoint rows of `out`
+        // and read the pool only.  The decode rows (sequences with one new
+        // row) run on the metadata's side stream, forked before the prefill
+        // launch and joined after, so that the HBM-bound split-K workgroups
+        // fill the wavefront slots the MFMA-bound prefill workgroups leave
+        // free.
         const hipStream_t st = static_cast<hipStream_t>(stream);
+        const bool overlap = m->decode_planned && mixed_overlap_enabled();
+        if (overlap) {
+            err = hipEventRecord(m->fork, st);
+            if (err == hipSuccess) err = hipStreamWaitEvent(m->side, m->fork, 0);
+            if (err != hipSuccess) return fail_device("prefill_attention", err, "stream fork");
+        }
         err = kernels::launch_prefill_mfma(pool->layer(layer), m->view, m->prefill_plan,
                                            static_cast<const uint16_t *>(queries),
                                            static_cast<uint16_t *>(out), heads, scale,
                                            pool->num_cus, st);
-        // Sequences with one new row (the decode rows of a mixed step).
         if (err == hipSuccess && m->decode_planned)
             err = kernels::launch_decode_mfma(pool->layer(layer), m->view, m->plan,
                                               static_cast<const uint16_t *>(queries),
                                               static_cast<uint16_t *>(out), heads, scale,
-                                              decode_waves(), st);
+                                              decode_waves(), overlap ? m->side : st);
+        if (overlap) {
+            // Joined whatever happened above, so the caller's stream never
+            // runs ahead of work left on the side stream.
+            hipError_t j = hipEventRecord(m->join, m->side);
+            if (j == hipSuccess) j = hipStreamWaitEvent(st, m->join, 0);
+            if (err == hipSuccess) err = j;
+        }
     } else {
         err = kernels::launch_attention_generic(
             pool->layer(layer), m->view, static_cast<const uint16_t *>(queries),

@@ -153,6 +153,10 @@ struct vo_step_meta {
     uint64_t buf_bytes = 0;
     hipEvent_t copy_done = nullptr;
     bool copy_pending = false;
+    // A mixed step's decode rows run on `side`, forked from and joined back
+    // into the caller's stream, beside the prefill chunks.
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
 
     // Split-K partials (fp32).
     float *d_part_acc = nullptr;
