@@ -80,6 +80,23 @@ class Workload:
         tab = int(np.sum(-(-keys // self.block_size))) * 4
         return kv + qo + tab
 
+    def decode_unique_bytes(self) -> int:
+        """decode_bytes with every physical block's keys counted once (the
+        HBM bytes when rows that alias a shared prefix hit it in cache):
+        per block, the most keys any sequence uses in it."""
+        keys = self.row_num_keys()
+        bs = self.block_size
+        used = {}
+        for s, t in enumerate(self.tables):
+            n = int(keys[s])
+            for i in range(-(-n // bs)):
+                b = int(t[i])
+                used[b] = max(used.get(b, 0), min(bs, n - i * bs))
+        kv = sum(used.values()) * self.kv_heads * self.head_dim * 2 * 2
+        qo = 2 * self.rows * self.heads * self.head_dim * 2
+        tab = int(np.sum(-(-keys // bs))) * 4
+        return kv + qo + tab
+
     def attention_flops(self) -> int:
         """Q.K^T plus P.V over each row's own keys (causal-aware)."""
         return int(self.row_num_keys().sum()) * self.heads * 4 * self.head_dim
