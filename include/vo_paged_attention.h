@@ -254,6 +254,15 @@ int32_t vo_step_meta_fix_launch(vo_step_meta *meta, uint64_t work_headroom,
 /* Back to packed uploads from the next upload on. */
 int32_t vo_step_meta_unfix_launch(vo_step_meta *meta);
 
+/* The split-K plan of the last upload (diagnostic; no counterpart in the
+ * reference, whose CPU backend has no launch plan): work items launched per
+ * KV head, split-K partials (one per (row, split)), and the row-packing
+ * factor P -- with P > 1, full splits of up to P rows that read the same
+ * physical blocks (a shared prefix) run as one work item.  VO_ERR_ARGUMENT
+ * when the last upload planned no decode rows. */
+int32_t vo_step_meta_decode_plan(const vo_step_meta *meta, uint64_t *work_items,
+                                 uint64_t *partials, uint32_t *pack);
+
 /* Upload only a slot list, for write_kv calls whose slots are not a step's
  * slot mapping (the reference's tests write ad-hoc ranges, cpu/tests.rs:210-230). */
 int32_t vo_step_meta_upload_slots(vo_step_meta *meta, const uint32_t *slots, uint64_t num_slots,

@@ -45,6 +45,14 @@ def _out(wl, backend):
     return backend.prefill_attention(wl.q, wl.pool, wl.layer, wl.meta)
 
 
+def _out_replanned(wl, backend):
+    """_out after uploading the metadata again, so that the launch plan is
+    rebuilt under the current VO_DECODE_* settings (an unchanged meta object
+    is otherwise not uploaded twice)."""
+    backend.step_meta(wl.pool).holds = None
+    return _out(wl, backend)
+
+
 # ---------------------------------------------------------------------------
 # reshape_and_cache + gather: bit-exact
 # ---------------------------------------------------------------------------
@@ -219,14 +227,56 @@ def test_decode_streaming_loads_bitwise_equal(vo, monkeypatch):
         outs = []
         for nt in ("0", "1"):
             monkeypatch.setenv("VO_DECODE_NT", nt)
-            outs.append(_bits(_out(wl, backend)))
+            outs.append(_bits(_out_replanned(wl, backend)))
         monkeypatch.delenv("VO_DECODE_NT")
-        auto = _bits(_out(wl, backend))
+        auto = _bits(_out_replanned(wl, backend))
         assert np.array_equal(outs[0], outs[1]), f"shared={shared}"
         assert np.array_equal(auto, outs[0]), f"shared={shared}"
         want = W.oracle_attention(orc, wl)
         got = backend.decode_attention(wl.q, wl.pool, 0, wl.meta).float().cpu().numpy()
         _assert_close(got, want, f"streaming shared={shared}")
+
+
+@pytest.mark.parametrize("hd,heads,kvh,split,waves", [
+    (128, 64, 8, "1024", "4"),  # cfg5's shape: group 8, two rows per item
+    (128, 32, 8, "512", "1"),   # group 4, four rows per item, no LDS merge
+    (64, 6, 2, "256", "2"),     # group 3, five rows per item, a short last pack
+])
+def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, waves):
+    """Rows whose full splits read the same physical blocks (an aliased
+    prefix) share one work item, each row in its own head columns of the
+    MFMA tile.  The outputs are bitwise those of the unpacked plan
+    (VO_DECODE_PACK=0) and within tolerance of the oracle; the plan really
+    packs: each of the two shared prefix splits of the 12 aliasing rows runs
+    as ceil(12 / P) items."""
+    monkeypatch.setenv("VO_DECODE_SPLIT", split)
+    monkeypatch.setenv("VO_DECODE_WAVES", waves)
+    _say(f"decode row packing hd={hd} heads={heads} kvh={kvh} split={split} waves={waves}")
+    L = int(split)
+    backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=8192,
+                            max_query_heads=heads)
+    shared = 2 * L
+    extra = [0, 1, 17, 100, L - 1, L, L + 5, 5, 2 * L + 3, 64, 700 % L, 31]
+    ctx = [shared + e for e in extra] + [3 * L, 50]
+    wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=16, num_blocks=4000, context_lens=ctx, seed=L + heads,
+                 shared_prefix=shared, shared_count=len(extra))
+    P = 16 // (heads // kvh)
+    parts = sum(-(-(c + 1) // L) for c in ctx)
+    meta = backend.step_meta(wl.pool)
+
+    monkeypatch.setenv("VO_DECODE_PACK", "0")
+    plain = _out_replanned(wl, backend)
+    assert meta.decode_plan() == (parts, parts, 1)
+    monkeypatch.delenv("VO_DECODE_PACK")
+    packed = _out_replanned(wl, backend)
+    packs = -(-len(extra) // P)
+    assert meta.decode_plan() == (parts - 2 * (len(extra) - packs), parts, P)
+    assert np.array_equal(_bits(packed), _bits(plain))
+    again = _out(wl, backend)
+    assert np.array_equal(_bits(again), _bits(packed))
+    want = W.oracle_attention(orc, wl)
+    _assert_close(packed.float().cpu().numpy(), want, f"packed hd={hd} H={heads}")
 
 
 def test_decode_cfg2_full_size(vo, gpu_backend):

@@ -154,6 +154,7 @@ SIGNATURES = {
     "vo_step_meta_upload_tokens": (ctypes.c_int32, [_vp, _u32p, _u64, _vp]),
     "vo_step_meta_fix_launch": (ctypes.c_int32, [_vp, _u64, _u64, _vp]),
     "vo_step_meta_unfix_launch": (ctypes.c_int32, [_vp]),
+    "vo_step_meta_decode_plan": (ctypes.c_int32, [_vp, _vp, _vp, _vp]),
     "vo_embed": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp]),
     "vo_rmsnorm": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp, _vp]),
     "vo_rmsnorm_last_rows": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp,
@@ -531,6 +532,14 @@ class StepMeta:
 
     def unfix_launch(self) -> None:
         _check(lib.vo_step_meta_unfix_launch(self._h))
+
+    def decode_plan(self) -> tuple:
+        """vo_step_meta_decode_plan: (work items, split-K partials, row-packing
+        factor) of the last upload's decode plan."""
+        w, p, k = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint32()
+        _check(lib.vo_step_meta_decode_plan(self._h, ctypes.byref(w), ctypes.byref(p),
+                                            ctypes.byref(k)))
+        return w.value, p.value, k.value
 
     def upload_slots(self, slots, stream=None) -> None:
         s = _u32(slots)

@@ -28,6 +28,15 @@
 // Workgroups are numbered KV head fastest, so the KV heads of one block are
 // read at about the same time.
 //
+// Row packing.  One row's group fills G of the MFMA tile's 16 head columns.
+// When the plan finds full splits of several rows over the same physical
+// blocks (aliased block-table entries: a shared prefix), one work item
+// serves up to 16 / G of them (`pack`; the others are listed in `mates`):
+// column h takes head h % G of row slot h / G.  The blocks are then read
+// once per pack instead of once per row, and since MFMA output columns and
+// the per-column softmax never mix, every row's result is bitwise the one
+// it gets unpacked.
+//
 // One 32-key chunk (two 16-key blocks b0, b1) of one wavefront:
 //   Q.K^T: S^T[key, h] = K[key, :] . Q[h, :] with v_mfma_f32_16x16x32_bf16,
 //          A = 16 keys x 32 dims of K (one 16-byte load per lane from the
@@ -192,11 +201,13 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                      const uint32_t *__restrict__ row_info, uint32_t split_keys,
                      const uint16_t *__restrict__ q, uint16_t *__restrict__ out,
                      float *__restrict__ part_acc, float *__restrict__ part_ml, uint32_t num_heads,
-                     uint32_t group, float scale_log2, const uint32_t *__restrict__ counts) {
+                     uint32_t group, float scale_log2, const uint32_t *__restrict__ counts,
+                     const uint32_t *__restrict__ mates, uint32_t pack) {
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
     constexpr uint32_t kTile = kBS * HD;
     __shared__ uint32_t s_table[kMaxSplitBlocks];
+    __shared__ uint32_t s_crow[16];
 
     const uint32_t item = blockIdx.x / kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads;
@@ -220,7 +231,6 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     const uint32_t *table = tables + table_off[seq];
     const uint32_t k_begin = split * split_keys;
     const uint32_t k_end = min(nk, k_begin + split_keys);
-    const uint32_t nsplit = (nk + split_keys - 1) / split_keys;
     const uint32_t nblk = (k_end - k_begin + kBS - 1) / kBS;
     const uint32_t lb0 = k_begin / kBS;
 
@@ -228,15 +238,29 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int h = lane & 15;  // head column of this lane
+    const int h = lane & 15;  // MFMA column of this lane
     const int g = lane >> 4;  // lane group: keys 8g..8g+7 of a chunk
-    const bool head_ok = h < static_cast<int>(group);
-    const uint32_t qhead = kvh * group + h;
+    // Column h holds query head kvh*group + hh of row slot h / group: slot 0
+    // is the item's own row, slot j > 0 its j-th mate (a row whose split
+    // reads the same blocks); columns past the pack stay zero.  MFMA output
+    // columns and the per-column softmax never mix, so a packed row gets the
+    // same bits as it would alone.
+    const uint32_t pslot = static_cast<uint32_t>(h) / group;
+    const uint32_t hh = static_cast<uint32_t>(h) - pslot * group;
+    uint32_t crow = kNoMate;
+    if (pslot == 0)
+        crow = row;
+    else if (pslot < pack)
+        crow = mates[(pack - 1) * item + pslot - 1];
+    const bool head_ok = crow != kNoMate;
+    const uint32_t qhead = kvh * group + hh;
+    if (wave == 0 && g == 0) s_crow[h] = crow;
 
     // Q^T operand: column h, dims 32*kk + 8g .. +7.
     bf16x8 qv[KK];
     {
-        const uint16_t *qp = q + (static_cast<uint64_t>(row) * num_heads + qhead) * HD + 8 * g;
+        const uint16_t *qp =
+            q + (static_cast<uint64_t>(head_ok ? crow : row) * num_heads + qhead) * HD + 8 * g;
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) qv[kk] = head_ok ? load_bf16x8(qp + 32 * kk) : bf16x8{};
     }
@@ -309,12 +333,14 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
 
-    const uint64_t part_base = static_cast<uint64_t>(row_info[2 * row] + split) * num_heads;
     if constexpr (W == 1) {
         if (head_ok) {
+            const uint32_t nsplit = (row_num_keys[crow] + split_keys - 1) / split_keys;
+            const uint64_t part_base = static_cast<uint64_t>(row_info[2 * crow] + split) * num_heads;
             if (nsplit == 1) {
                 const float inv = 1.0f / l_run;
-                uint16_t *op = out + out_base + static_cast<uint64_t>(qhead) * HD + 4 * g;
+                uint16_t *op = out + static_cast<uint64_t>(crow) * num_heads * HD +
+                               static_cast<uint64_t>(qhead) * HD + 4 * g;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
                     u32x2 packed;
@@ -340,38 +366,44 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         extern __shared__ float smem[];
         float *sm_m = smem;             // [W][16]
         float *sm_l = sm_m + W * 16;    // [W][16]
-        float *sm_acc = sm_l + W * 16;  // [W][group][HD]
+        float *sm_acc = sm_l + W * 16;  // [W][cols][HD]
+        const uint32_t cols = pack * group;
         if (head_ok) {
             if (g == 0) {
                 sm_m[wave * 16 + h] = m_run;
                 sm_l[wave * 16 + h] = l_run;
             }
-            float *ap = sm_acc + (static_cast<uint32_t>(wave) * group + h) * HD + 4 * g;
+            float *ap = sm_acc + (static_cast<uint32_t>(wave) * cols + h) * HD + 4 * g;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = acc[dt];
         }
         __syncthreads();
-        for (uint32_t idx = threadIdx.x; idx < group * HD; idx += 64 * W) {
-            const uint32_t hh = idx / HD;
+        for (uint32_t idx = threadIdx.x; idx < cols * HD; idx += 64 * W) {
+            const uint32_t col = idx / HD;
             const uint32_t d = idx % HD;
+            const uint32_t r = s_crow[col];
+            if (r == kNoMate) continue;  // a short pack
             float mx = -INFINITY;
 #pragma unroll
-            for (int w = 0; w < W; ++w) mx = fmaxf(mx, sm_m[w * 16 + hh]);
+            for (int w = 0; w < W; ++w) mx = fmaxf(mx, sm_m[w * 16 + col]);
             float num = 0.0f, den = 0.0f;
 #pragma unroll
             for (int w = 0; w < W; ++w) {
-                const float mw = sm_m[w * 16 + hh];
+                const float mw = sm_m[w * 16 + col];
                 if (mw != -INFINITY) {
                     const float e = __builtin_amdgcn_exp2f(mw - mx);
-                    num += e * sm_acc[(w * group + hh) * HD + d];
-                    den += e * sm_l[w * 16 + hh];
+                    num += e * sm_acc[(w * cols + col) * HD + d];
+                    den += e * sm_l[w * 16 + col];
                 }
             }
-            const uint32_t qh = kvh * group + hh;
+            const uint32_t qh = kvh * group + (col % group);
+            const uint32_t nsplit = (row_num_keys[r] + split_keys - 1) / split_keys;
             if (nsplit == 1) {
-                out[out_base + static_cast<uint64_t>(qh) * HD + d] = f32_to_bf16_bits(num / den);
+                out[static_cast<uint64_t>(r) * num_heads * HD + static_cast<uint64_t>(qh) * HD + d] =
+                    f32_to_bf16_bits(num / den);
             } else {
-                const uint64_t part = part_base + qh;
+                const uint64_t part =
+                    static_cast<uint64_t>(row_info[2 * r] + split) * num_heads + qh;
                 part_acc[part * HD + d] = num;
                 if (d == 0) {
                     part_ml[2 * part] = mx;
@@ -458,7 +490,9 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                         const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
                         hipStream_t stream) {
     const uint32_t group = num_heads / pool.kv_heads;
-    const size_t smem = (W == 1) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * group * HD) * 4;
+    const uint32_t pack = plan.pack ? plan.pack : 1;
+    if (pack * group > 16 || (pack > 1 && plan.mates == nullptr)) return hipErrorInvalidValue;
+    const size_t smem = (W == 1) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * pack * group * HD) * 4;
     const uint64_t grid = static_cast<uint64_t>(plan.launch_work) * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
@@ -466,7 +500,7 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                        dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
                        meta.tables, meta.row_seq, meta.row_num_keys, plan.work, plan.row_info,
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
-                       scale_log2, plan.counts);
+                       scale_log2, plan.counts, plan.mates, pack);
     return hipGetLastError();
 }
 

@@ -162,7 +162,16 @@ struct DecodePlan {
     const uint32_t *counts;       // device [2]: num_work, num_reduce_rows; the kernels stop there
     uint32_t launch_work;         // work items launched (>= num_work; = num_work unless fixed)
     uint32_t launch_reduce;       // reduce rows launched (>= num_reduce_rows)
+    // Row packing: item i also serves the rows mates[(pack-1)*i .. +pack-2]
+    // (kNoMate where its pack is short), rows whose split reads the same
+    // blocks; the pack * group head columns fit one 16-column MFMA tile.
+    // pack == 1: no mates (mates may be null).
+    const uint32_t *mates;
+    uint32_t pack;
 };
+
+constexpr uint32_t kNoMate = 0xffffffffu;
+
 
 // True when the MFMA decode kernel covers this shape.
 bool decode_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t group);

@@ -351,6 +351,67 @@ bool decode_streaming(vo_step_meta *m) {
 // Rows with zero keys still get one work item (it writes the zero output).
 uint64_t row_splits(uint64_t keys, uint64_t L) { return keys ? (keys + L - 1) / L : 1; }
 
+// Row packing.  The split kernel computes 16 head columns per MFMA, of which
+// one row's KV-head group uses G = query heads / KV heads.  Full splits of
+// different rows that read the same physical blocks (aliased block-table
+// entries: a shared prefix) go to one workgroup, up to 16 / G rows, so those
+// blocks are read once per pack instead of once per row.  Each row keeps its
+// own columns, softmax and partial, so its result is bitwise the one it gets
+// unpacked.  The limit uses the largest group the metadata admits, so any
+// call's group fits; the staging buffer is sized for it.  VO_DECODE_PACK=0
+// turns packing off (decode_pack_factor).
+uint32_t decode_pack_limit(const vo_step_meta *m) {
+    if (m->kv_heads == 0) return 1;
+    const uint64_t group = std::max<uint64_t>(1, (m->max_heads + m->kv_heads - 1) / m->kv_heads);
+    const uint64_t p = 16 / group;
+    return p >= 2 ? static_cast<uint32_t>(p) : 1u;
+}
+
+uint32_t decode_pack_factor(const vo_step_meta *m) {
+    return env_int("VO_DECODE_PACK", 1) == 0 ? 1u : decode_pack_limit(m);
+}
+
+// Packs work[0 .. nfull) (full splits, (row, split) pairs) in place: items
+// with the same split index over the same block list join the first open
+// pack of that list (its leader keeps the item's place, the others become
+// its mates).  Returns the number of packed items; mates gets P - 1 entries
+// per packed item, kNoMate where a pack is short.
+uint64_t pack_full_splits(vo_step_meta *m, uint32_t *work, uint64_t nfull, uint64_t L,
+                          uint32_t P, uint32_t *mates) {
+    const uint64_t nb = L / m->block_size;
+    auto blocks_of = [&](uint32_t row, uint32_t split) {
+        return m->tables.data() + m->table_off[m->row_seq[row]] + split * nb;
+    };
+    m->pack_open.clear();
+    m->pack_fill.clear();
+    uint64_t n = 0;
+    for (uint64_t f = 0; f < nfull; ++f) {
+        const uint32_t row = work[2 * f], split = work[2 * f + 1];
+        const uint32_t *b = blocks_of(row, split);
+        uint64_t hsh = 0xcbf29ce484222325ull ^ split;  // FNV-1a over (split, blocks)
+        for (uint64_t i = 0; i < nb; ++i) hsh = (hsh ^ b[i]) * 0x100000001b3ull;
+        auto it = m->pack_open.find(hsh);
+        if (it != m->pack_open.end()) {
+            const uint32_t lead = it->second;
+            const uint32_t lrow = work[2 * lead];
+            if (work[2 * lead + 1] == split &&
+                std::memcmp(blocks_of(lrow, split), b, nb * sizeof(uint32_t)) == 0) {
+                mates[(P - 1) * lead + m->pack_fill[lead] - 1] = row;
+                if (++m->pack_fill[lead] == P) m->pack_open.erase(it);
+                continue;
+            }
+        }
+        // A new pack (a hash collision just starts another one).
+        work[2 * n] = row;
+        work[2 * n + 1] = split;
+        std::fill(mates + (P - 1) * n, mates + (P - 1) * (n + 1), kernels::kNoMate);
+        m->pack_fill.push_back(1);
+        m->pack_open[hsh] = static_cast<uint32_t>(n);
+        ++n;
+    }
+    return n;
+}
+
 // Split-K plan over the rows listed in `rows` (every row of the step when
 // rows is null).  Rows outside the plan get row_info (0, 0).
 vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32_t> *rows) {
@@ -387,6 +448,16 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     }
     m->tail_items.clear();
     uint64_t f = 0;
+    const bool streaming = pk.fixed() ? m->fixed.streaming : decode_streaming(m);
+    // Packing needs shared blocks, so a streaming plan never packs; a fixed
+    // launch keeps one item per (row, split).
+    const uint32_t P = (pk.fixed() || streaming || L % m->block_size != 0) ? 1u : decode_pack_factor(m);
+    uint32_t *mates = nullptr;
+    m->plan.mates = nullptr;
+    if (P > 1) {
+        mates = pk.add(kRegMates, (P - 1) * parts, &dp);
+        m->plan.mates = dp;
+    }
     for (uint64_t i = 0; i < R; ++i) {
         const uint64_t r = row_at(i);
         const uint64_t nk = m->row_num_keys[r];
@@ -398,31 +469,36 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
             m->tail_items.push_back({static_cast<uint32_t>(nk % L), static_cast<uint32_t>(r),
                                      static_cast<uint32_t>(nk / L)});
     }
+    if (P > 1) f = pack_full_splits(m, work, f, L, P, mates);
     std::stable_sort(m->tail_items.begin(), m->tail_items.end(),
                      [](const TailItem &a, const TailItem &b) { return a.keys > b.keys; });
     for (const TailItem &t : m->tail_items) {
         work[2 * f] = t.row;
         work[2 * f + 1] = t.split;
+        if (P > 1) std::fill(mates + (P - 1) * f, mates + (P - 1) * (f + 1), kernels::kNoMate);
         ++f;
     }
-    m->plan.num_work = static_cast<uint32_t>(parts);
+    const uint64_t num_work = f;  // = parts unless packed
+    m->decode_parts = parts;
+    m->plan.pack = P;
+    m->plan.num_work = static_cast<uint32_t>(num_work);
     m->plan.num_reduce_rows = static_cast<uint32_t>(nred);
     m->plan.split_keys = static_cast<uint32_t>(L);
     m->plan.part_acc = m->d_part_acc;
     m->plan.part_ml = m->d_part_ml;
-    m->h_counts[0] = static_cast<uint32_t>(parts);
+    m->h_counts[0] = static_cast<uint32_t>(num_work);
     m->h_counts[1] = static_cast<uint32_t>(nred);
     m->plan.counts = m->d_counts;
     if (pk.fixed()) {
         // The same launches every step: capacity-sized grids, the kernels stop
         // at the counts; the load policy stays the one fixed (it changes no
         // arithmetic).
-        m->plan.streaming = m->fixed.streaming;
+        m->plan.streaming = streaming;
         m->plan.launch_work = static_cast<uint32_t>(m->fixed.work_cap);
         m->plan.launch_reduce = static_cast<uint32_t>(m->fixed.seqs);
     } else {
-        m->plan.streaming = decode_streaming(m);
-        m->plan.launch_work = static_cast<uint32_t>(parts);
+        m->plan.streaming = streaming;
+        m->plan.launch_work = static_cast<uint32_t>(num_work);
         m->plan.launch_reduce = static_cast<uint32_t>(nred);
     }
     m->decode_planned = true;
@@ -580,7 +656,8 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
                           + 2 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
                           + max_seqs                                         // last rows
-                          + 9 * 64;                                          // alignment slack
+                          + (decode_pack_limit(m) - 1) * m->max_parts        // row-packing mates
+                          + 10 * 64;                                         // alignment slack
     m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
     hipError_t err = hipMalloc(reinterpret_cast<void **>(&m->d_buf), m->buf_bytes);
     if (err == hipSuccess)
@@ -760,13 +837,13 @@ extern "C" int32_t vo_step_meta_fix_launch(vo_step_meta *m, uint64_t work_headro
     f.on = true;
     f.seqs = m->num_seqs;
     f.entries_cap = std::min<uint64_t>(m->tables.size() + entry_headroom, m->max_entries);
-    f.work_cap = std::min<uint64_t>(m->plan.num_work + work_headroom, m->max_parts);
+    f.work_cap = std::min<uint64_t>(m->decode_parts + work_headroom, m->max_parts);
     f.has_positions = !m->positions.empty() || (m->num_rows == 0 && m->has_positions);
     f.streaming = m->plan.streaming;
     const uint64_t S = f.seqs;
     const uint64_t caps[kNumRegions] = {
         2, S + 1, f.entries_cap, S, S, f.has_positions ? S : 0, S, 3 * S,
-        2 * f.work_cap, 2 * S, S, S, 0};
+        2 * f.work_cap, 2 * S, S, S, 0, 0};
     uint64_t off = 0;
     for (int r = 0; r < kNumRegions; ++r) {
         off = align_up(off, 256);
@@ -789,6 +866,17 @@ extern "C" int32_t vo_step_meta_fix_launch(vo_step_meta *m, uint64_t work_headro
         row_keys.data(), stream);
     if (rc != VO_OK) m->fixed = saved;
     return rc;
+}
+
+extern "C" int32_t vo_step_meta_decode_plan(const vo_step_meta *m, uint64_t *work_items,
+                                            uint64_t *partials, uint32_t *pack) {
+    if (!m || !work_items || !partials || !pack) return fail_argument("decode_plan", "null argument");
+    if (!m->decode_planned) return fail_argument("decode_plan", "the last upload has no decode plan");
+    *work_items = m->plan.num_work;
+    *partials = m->decode_parts;
+    *pack = m->plan.pack ? m->plan.pack : 1;
+    clear_error();
+    return VO_OK;
 }
 
 extern "C" int32_t vo_step_meta_unfix_launch(vo_step_meta *m) {

@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "kernels/vo_kernels.hpp"
@@ -74,6 +75,7 @@ enum Region {
     kRegReduceRows,
     kRegLastRows,
     kRegPrefillWork,
+    kRegMates,
     kNumRegions
 };
 
@@ -171,6 +173,9 @@ struct vo_step_meta {
     std::vector<uint8_t> block_seen;   // scratch of plan_decode: one byte per physical block
     std::vector<uint64_t> seq_keys;    // scratch of plan_decode: keys read per sequence
     std::vector<uint32_t> decode_rows; // rows of a prefill step planned on the decode kernel
+    uint64_t decode_parts = 0;         // split-K partials of the plan (work items before packing)
+    std::unordered_map<uint64_t, uint32_t> pack_open;  // scratch of plan_decode: open packs by hash
+    std::vector<uint32_t> pack_fill;                   // scratch of plan_decode: rows per pack
     vo::kernels::PrefillPlan prefill_plan{};
     bool prefill_planned = false;  // rows are regular: one contiguous run per sequence
 
