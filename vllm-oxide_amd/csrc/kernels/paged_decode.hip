@@ -12,11 +12,14 @@
 // Work split.  The keys of each row are cut into splits of `split_keys`
 // (a multiple of 32, at most kMaxSplitKeys).  Workgroup (item, k) owns one
 // (row, split) for one KV head and all G heads of its group, so every K/V
-// byte is read from HBM once: the algorithmic minimum.  The workgroup first
-// copies its split's block-table slice into LDS; its W wavefronts then take
-// the split's 32-key chunks round robin, each wavefront keeping the next
-// chunk's 16 loads in flight while it computes the current one (two register
-// buffers).  The wavefronts merge through LDS at the end.  A row with one
+// byte is read from HBM once: the algorithmic minimum.  An item is one
+// 16-byte record (row, split, where the split's block ids start, keys), so
+// the workgroup starts its loads after one dependent read.  Its W wavefronts
+// take the split's 32-key chunks round robin; block ids are wave-uniform and
+// come from scalar loads.  Each wavefront issues all 16 loads of its next
+// chunk before it waits for the current one (two register buffers), so two
+// chunks are in flight per wavefront.  The wavefronts merge through LDS at
+// the end.  A row with one
 // split writes its bf16 output directly; otherwise the workgroup writes an
 // fp32 partial (m, l, acc[head_dim]) per head, and decode_reduce_kernel
 // merges them:
@@ -73,7 +76,6 @@ namespace {
 
 constexpr int kBS = 16;     // block size of the MFMA path
 constexpr int kChunk = 32;  // keys per wavefront iteration
-constexpr int kMaxSplitBlocks = kMaxSplitKeys / kBS;
 
 __device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -192,12 +194,15 @@ __device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 *qv, bo
     }
 }
 
+// Keeps the scheduler from moving instructions across this point: the next
+// chunk's loads are all issued before the current chunk's first wait.
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 template <int HD, int W, bool NT>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void
 decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
-                     uint32_t kv_heads, const uint32_t *__restrict__ table_off,
-                     const uint32_t *__restrict__ tables, const uint32_t *__restrict__ row_seq,
-                     const uint32_t *__restrict__ row_num_keys, const uint32_t *__restrict__ work,
+                     uint32_t kv_heads, const uint32_t *__restrict__ tables,
+                     const uint32_t *__restrict__ work,
                      const uint32_t *__restrict__ row_info, uint32_t split_keys,
                      const uint16_t *__restrict__ q, uint16_t *__restrict__ out,
                      float *__restrict__ part_acc, float *__restrict__ part_ml, uint32_t num_heads,
@@ -206,17 +211,19 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
     constexpr uint32_t kTile = kBS * HD;
-    __shared__ uint32_t s_table[kMaxSplitBlocks];
-    __shared__ uint32_t s_crow[16];
+    __shared__ uint32_t s_col[3][16];  // per column: row, first partial, splits
 
     const uint32_t item = blockIdx.x / kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads;
-    // The grid may be sized for more work than this step has (fixed launch
-    // shapes); the step's own count is on the device.
+    // The item's record loads beside the step's count: every launched item
+    // has a readable record.  The grid may be sized for more work than this
+    // step has (fixed launch shapes); the step's own count is on the device.
+    const u32x4 rec = *reinterpret_cast<const u32x4 *>(work + 4 * static_cast<uint64_t>(item));
     if (item >= counts[0]) return;
-    const uint32_t row = work[2 * item];
-    const uint32_t split = work[2 * item + 1];
-    const uint32_t nk = row_num_keys[row];
+    const uint32_t row = rec[0];
+    const uint32_t split = rec[1];
+    const uint32_t *table = tables + rec[2];  // this split's block ids
+    const uint32_t nk = rec[3];
     const uint64_t out_base = static_cast<uint64_t>(row) * num_heads * HD;
 
     if (nk == 0) {
@@ -227,19 +234,28 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         return;
     }
 
-    const uint32_t seq = row_seq[row];
-    const uint32_t *table = tables + table_off[seq];
     const uint32_t k_begin = split * split_keys;
     const uint32_t k_end = min(nk, k_begin + split_keys);
     const uint32_t nblk = (k_end - k_begin + kBS - 1) / kBS;
-    const uint32_t lb0 = k_begin / kBS;
-
-    for (uint32_t i = threadIdx.x; i < nblk; i += 64 * W) s_table[i] = table[lb0 + i];
+    const uint32_t nchunks = (k_end - k_begin + kChunk - 1) / kChunk;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane & 15;  // MFMA column of this lane
     const int g = lane >> 4;  // lane group: keys 8g..8g+7 of a chunk
+
+    LaneMap lm;
+    {
+        const int m = lane & 15;
+        lm.k_off = (8 * ((m >> 2) & 1) + (m & 3)) * 32 + 8 * g;
+        lm.k_hi = m >= 8;
+        lm.v_off = m * kBS + 8 * (g & 1);
+        lm.v_hi = g >= 2;
+    }
+    const uint64_t block_stride = static_cast<uint64_t>(kv_heads) * kTile;
+    const uint16_t *k_head = k_pool + static_cast<uint64_t>(kvh) * kTile;
+    const uint16_t *v_head = v_pool + static_cast<uint64_t>(kvh) * kTile;
+
     // Column h holds query head kvh*group + hh of row slot h / group: slot 0
     // is the item's own row, slot j > 0 its j-th mate (a row whose split
     // reads the same blocks); columns past the pack stay zero.  MFMA output
@@ -254,7 +270,6 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         crow = mates[(pack - 1) * item + pslot - 1];
     const bool head_ok = crow != kNoMate;
     const uint32_t qhead = kvh * group + hh;
-    if (wave == 0 && g == 0) s_crow[h] = crow;
 
     // Q^T operand: column h, dims 32*kk + 8g .. +7.
     bf16x8 qv[KK];
@@ -264,18 +279,29 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) qv[kk] = head_ok ? load_bf16x8(qp + 32 * kk) : bf16x8{};
     }
+    // The column's output place (first partial, splits), loaded now so that
+    // the end of the item waits on no load.
+    u32x2 cinfo = {0u, 0u};
+    if (head_ok) cinfo = *reinterpret_cast<const u32x2 *>(row_info + 2 * static_cast<uint64_t>(crow));
 
-    LaneMap lm;
-    {
-        const int m = lane & 15;
-        lm.k_off = (8 * ((m >> 2) & 1) + (m & 3)) * 32 + 8 * g;
-        lm.k_hi = m >= 8;
-        lm.v_off = m * kBS + 8 * (g & 1);
-        lm.v_hi = g >= 2;
-    }
-    const uint64_t block_stride = static_cast<uint64_t>(kv_heads) * kTile;
-    const uint16_t *k_head = k_pool + static_cast<uint64_t>(kvh) * kTile;
-    const uint16_t *v_head = v_pool + static_cast<uint64_t>(kvh) * kTile;
+    // Block ids of chunk cc: wave-uniform, so scalar loads from the table
+    // (no LDS copy, no VGPR).  Load order: mates, Q and column info, first
+    // chunk, so that each wait for a value (vmcnt counts in issue order)
+    // leaves the later loads in flight.  Every wave issues its first chunk,
+    // a wave without one from the split's last block, so that no branch
+    // leaves the compiler's wait counting unsure.
+    auto load = [&](Chunk<HD> &r, uint32_t cc) {
+        const uint32_t b0 = min(2 * cc, nblk - 1);
+        const uint32_t p0 = table[b0];
+        const uint32_t p1 = (b0 + 1 < nblk) ? table[b0 + 1] : p0;
+        load_chunk<HD, NT>(r, k_head, v_head, block_stride, p0, p1, lm);
+        issue_fence();
+    };
+    Chunk<HD> bufA, bufB;
+    // This wavefront's chunks: wave + k W for k < mine.
+    const uint32_t mine = nchunks > static_cast<uint32_t>(wave) ? (nchunks - wave + W - 1) / W : 0;
+    auto chunk = [&](uint32_t k) { return static_cast<uint32_t>(wave) + k * W; };
+    load(bufA, chunk(0));
 
     float m_run = -INFINITY;
     float l_run = 0.0f;
@@ -283,50 +309,35 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    __syncthreads();  // s_table ready
-
-    const uint32_t nchunks = (k_end - k_begin + kChunk - 1) / kChunk;
-    auto phys = [&](uint32_t c, uint32_t &p0, uint32_t &p1) {
-        p0 = s_table[2 * c];
-        p1 = (2 * c + 1 < nblk) ? s_table[2 * c + 1] : p0;
-    };
-    auto run = [&](Chunk<HD> &r, uint32_t c) {
-        const uint32_t j0 = k_begin + c * kChunk;
-        const bool tail = j0 + kChunk > k_end;
+    // A chunk computed inside the loop has a successor, so it is full: only
+    // the chunks computed at the loop's exits can be the split's tail, and
+    // only they carry the masking code.
+    auto run = [&](Chunk<HD> &r, uint32_t cc, bool may_tail) {
+        const uint32_t j0 = k_begin + cc * kChunk;
+        const bool tail = may_tail && j0 + kChunk > k_end;
         const int nv = max(0, min(8, static_cast<int>(k_end) - static_cast<int>(j0 + 8 * g)));
         compute_chunk<HD>(r, qv, tail, nv, scale_log2, m_run, l_run, acc);
     };
 
-    // Two register buffers: the loads of chunk c + W are in flight while
-    // chunk c is computed.  Each "load next; compute current" pair is
-    // straight-line code, so the compiler's wait before the compute covers
-    // only the current chunk's loads; the last chunk is computed without a
-    // prefetch.
-    Chunk<HD> bufA, bufB;
-    auto load = [&](Chunk<HD> &r, uint32_t cc) {
-        uint32_t p0, p1;
-        phys(cc, p0, p1);
-        load_chunk<HD, NT>(r, k_head, v_head, block_stride, p0, p1, lm);
-    };
-    uint32_t c = wave;
-    if (c < nchunks) {
-        load(bufA, c);
-        for (;;) {
-            if (c + W >= nchunks) {
-                run(bufA, c);
-                break;
-            }
-            load(bufB, c + W);
-            run(bufA, c);
-            c += W;
-            if (c + W >= nchunks) {
-                run(bufB, c);
-                break;
-            }
-            load(bufA, c + W);
-            run(bufB, c);
-            c += W;
-        }
+    // Two register buffers: the loads of chunk k + 1 are all issued (the
+    // fence in `load`) before the first wait for chunk k, so each wavefront
+    // has two chunks in flight while it waits.  The loop has one exit and
+    // the last one or two chunks follow it: with an early exit inside the
+    // loop, the control-flow structurizer routes that exit back through the
+    // loop header, where the compiler then waits for every load in flight.
+    uint32_t k = 0;
+    for (; k + 2 < mine; k += 2) {
+        load(bufB, chunk(k + 1));
+        run(bufA, chunk(k), false);
+        load(bufA, chunk(k + 2));
+        run(bufB, chunk(k + 1), false);
+    }
+    if (k + 1 < mine) {
+        load(bufB, chunk(k + 1));
+        run(bufA, chunk(k), false);
+        run(bufB, chunk(k + 1), true);
+    } else if (k < mine) {
+        run(bufA, chunk(k), true);
     }
 
     // The running sums are per lane group; the max is already per head.
@@ -335,8 +346,8 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
 
     if constexpr (W == 1) {
         if (head_ok) {
-            const uint32_t nsplit = (row_num_keys[crow] + split_keys - 1) / split_keys;
-            const uint64_t part_base = static_cast<uint64_t>(row_info[2 * crow] + split) * num_heads;
+            const uint32_t nsplit = cinfo[1];
+            const uint64_t part_base = static_cast<uint64_t>(cinfo[0] + split) * num_heads;
             if (nsplit == 1) {
                 const float inv = 1.0f / l_run;
                 uint16_t *op = out + static_cast<uint64_t>(crow) * num_heads * HD +
@@ -368,6 +379,11 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         float *sm_l = sm_m + W * 16;    // [W][16]
         float *sm_acc = sm_l + W * 16;  // [W][cols][HD]
         const uint32_t cols = pack * group;
+        if (wave == 0 && g == 0) {
+            s_col[0][h] = crow;
+            s_col[1][h] = cinfo[0];
+            s_col[2][h] = cinfo[1];
+        }
         if (head_ok) {
             if (g == 0) {
                 sm_m[wave * 16 + h] = m_run;
@@ -381,7 +397,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         for (uint32_t idx = threadIdx.x; idx < cols * HD; idx += 64 * W) {
             const uint32_t col = idx / HD;
             const uint32_t d = idx % HD;
-            const uint32_t r = s_crow[col];
+            const uint32_t r = s_col[0][col];
             if (r == kNoMate) continue;  // a short pack
             float mx = -INFINITY;
 #pragma unroll
@@ -397,13 +413,12 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                 }
             }
             const uint32_t qh = kvh * group + (col % group);
-            const uint32_t nsplit = (row_num_keys[r] + split_keys - 1) / split_keys;
+            const uint32_t nsplit = s_col[2][col];
             if (nsplit == 1) {
                 out[static_cast<uint64_t>(r) * num_heads * HD + static_cast<uint64_t>(qh) * HD + d] =
                     f32_to_bf16_bits(num / den);
             } else {
-                const uint64_t part =
-                    static_cast<uint64_t>(row_info[2 * r] + split) * num_heads + qh;
+                const uint64_t part = static_cast<uint64_t>(s_col[1][col] + split) * num_heads + qh;
                 part_acc[part * HD + d] = num;
                 if (d == 0) {
                     part_ml[2 * part] = mx;
@@ -497,8 +512,8 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
     hipLaunchKernelGGL((decode_splitk_kernel<HD, W, NT>), dim3(static_cast<uint32_t>(grid)),
-                       dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
-                       meta.tables, meta.row_seq, meta.row_num_keys, plan.work, plan.row_info,
+                       dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.tables,
+                       plan.work, plan.row_info,
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
                        scale_log2, plan.counts, plan.mates, pack);
     return hipGetLastError();

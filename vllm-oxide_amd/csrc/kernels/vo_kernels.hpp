@@ -149,7 +149,9 @@ constexpr uint32_t kMaxSplitKeys = 4096;
 
 // Split-K work plan for the MFMA decode kernel.
 struct DecodePlan {
-    const uint32_t *work;         // [num_work][2]: (row, split); a zero-key row has one item
+    const uint32_t *work;         // [num_work][4]: (row, split, index of the split's first
+                                  // block id in `tables`, the row's keys); 16-byte aligned,
+                                  // launch_work records readable; a zero-key row has one item
     const uint32_t *row_info;     // [T][2]: (first partial index, number of splits); (0, 0) for
                                   // rows the plan does not cover
     const uint32_t *reduce_rows;  // [num_reduce_rows]: rows with more than one split

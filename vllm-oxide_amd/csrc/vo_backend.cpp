@@ -371,7 +371,8 @@ uint32_t decode_pack_factor(const vo_step_meta *m) {
     return env_int("VO_DECODE_PACK", 1) == 0 ? 1u : decode_pack_limit(m);
 }
 
-// Packs work[0 .. nfull) (full splits, (row, split) pairs) in place: items
+// Packs work[0 .. nfull) (full splits; (row, split) in the first two words
+// of each record) in place: items
 // with the same split index over the same block list join the first open
 // pack of that list (its leader keeps the item's place, the others become
 // its mates).  Returns the number of packed items; mates gets P - 1 entries
@@ -386,15 +387,15 @@ uint64_t pack_full_splits(vo_step_meta *m, uint32_t *work, uint64_t nfull, uint6
     m->pack_fill.clear();
     uint64_t n = 0;
     for (uint64_t f = 0; f < nfull; ++f) {
-        const uint32_t row = work[2 * f], split = work[2 * f + 1];
+        const uint32_t row = work[4 * f], split = work[4 * f + 1];
         const uint32_t *b = blocks_of(row, split);
         uint64_t hsh = 0xcbf29ce484222325ull ^ split;  // FNV-1a over (split, blocks)
         for (uint64_t i = 0; i < nb; ++i) hsh = (hsh ^ b[i]) * 0x100000001b3ull;
         auto it = m->pack_open.find(hsh);
         if (it != m->pack_open.end()) {
             const uint32_t lead = it->second;
-            const uint32_t lrow = work[2 * lead];
-            if (work[2 * lead + 1] == split &&
+            const uint32_t lrow = work[4 * lead];
+            if (work[4 * lead + 1] == split &&
                 std::memcmp(blocks_of(lrow, split), b, nb * sizeof(uint32_t)) == 0) {
                 mates[(P - 1) * lead + m->pack_fill[lead] - 1] = row;
                 if (++m->pack_fill[lead] == P) m->pack_open.erase(it);
@@ -402,8 +403,8 @@ uint64_t pack_full_splits(vo_step_meta *m, uint32_t *work, uint64_t nfull, uint6
             }
         }
         // A new pack (a hash collision just starts another one).
-        work[2 * n] = row;
-        work[2 * n + 1] = split;
+        work[4 * n] = row;
+        work[4 * n + 1] = split;
         std::fill(mates + (P - 1) * n, mates + (P - 1) * (n + 1), kernels::kNoMate);
         m->pack_fill.push_back(1);
         m->pack_open[hsh] = static_cast<uint32_t>(n);
@@ -424,7 +425,7 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     if (parts > m->max_parts) return fail_capacity("split-K partials per step", parts, m->max_parts);
 
     const uint32_t *dp;
-    uint32_t *work = pk.add(kRegWork, 2 * parts, &dp);
+    uint32_t *work = pk.add(kRegWork, 4 * parts, &dp);
     m->plan.work = dp;
     uint32_t *row_info = pk.add(kRegRowInfo, 2 * T, &dp);
     m->plan.row_info = dp;
@@ -462,8 +463,8 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
         const uint64_t r = row_at(i);
         const uint64_t nk = m->row_num_keys[r];
         for (uint64_t sp = 0; sp < nk / L; ++sp, ++f) {
-            work[2 * f] = static_cast<uint32_t>(r);
-            work[2 * f + 1] = static_cast<uint32_t>(sp);
+            work[4 * f] = static_cast<uint32_t>(r);
+            work[4 * f + 1] = static_cast<uint32_t>(sp);
         }
         if (nk % L != 0 || nk == 0)
             m->tail_items.push_back({static_cast<uint32_t>(nk % L), static_cast<uint32_t>(r),
@@ -473,12 +474,21 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     std::stable_sort(m->tail_items.begin(), m->tail_items.end(),
                      [](const TailItem &a, const TailItem &b) { return a.keys > b.keys; });
     for (const TailItem &t : m->tail_items) {
-        work[2 * f] = t.row;
-        work[2 * f + 1] = t.split;
+        work[4 * f] = t.row;
+        work[4 * f + 1] = t.split;
         if (P > 1) std::fill(mates + (P - 1) * f, mates + (P - 1) * (f + 1), kernels::kNoMate);
         ++f;
     }
     const uint64_t num_work = f;  // = parts unless packed
+    // The rest of each record: where the split's block ids start in the
+    // tables, and the (leading) row's key count.
+    for (uint64_t i = 0; i < num_work; ++i) {
+        const uint32_t row = work[4 * i];
+        const uint64_t split = work[4 * i + 1];
+        work[4 * i + 2] =
+            static_cast<uint32_t>(m->table_off[m->row_seq[row]] + split * L / m->block_size);
+        work[4 * i + 3] = m->row_num_keys[row];
+    }
     m->decode_parts = parts;
     m->plan.pack = P;
     m->plan.num_work = static_cast<uint32_t>(num_work);
@@ -653,7 +663,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
                           + max_rows                                         // write slots
                           + 3 * max_rows                                     // write plan
                           + max_rows                                         // positions
-                          + 2 * m->max_parts + 3 * max_rows                  // decode plan
+                          + 4 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
                           + max_seqs                                         // last rows
                           + (decode_pack_limit(m) - 1) * m->max_parts        // row-packing mates
@@ -843,7 +853,7 @@ extern "C" int32_t vo_step_meta_fix_launch(vo_step_meta *m, uint64_t work_headro
     const uint64_t S = f.seqs;
     const uint64_t caps[kNumRegions] = {
         2, S + 1, f.entries_cap, S, S, f.has_positions ? S : 0, S, 3 * S,
-        2 * f.work_cap, 2 * S, S, S, 0, 0};
+        4 * f.work_cap, 2 * S, S, S, 0, 0};
     uint64_t off = 0;
     for (int r = 0; r < kNumRegions; ++r) {
         off = align_up(off, 256);
