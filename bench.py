@@ -170,7 +170,7 @@ def bench_decode(vo, W, orc, args, cfg):
             "keys_total": int(wl.row_num_keys().sum()),
             "step": "write_kv(new tokens) + decode_attention (split-K + reduce)",
             "layers_rotated": layers,
-            "split_keys": int(os.environ.get("VO_DECODE_SPLIT", "1024")),
+            "split_keys": int(os.environ.get("VO_DECODE_SPLIT", "2048")),  # the backend's default
         },
         "tokens_per_s": round(S / sec, 1),
         "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),

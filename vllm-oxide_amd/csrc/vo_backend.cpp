@@ -313,7 +313,11 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
 // order, and how the partials merge -- is the same alone or in any batch:
 // the reference's batch-invariance invariant (CLAUDE.md "Batch invariance",
 // model.rs:539-584).  VO_DECODE_SPLIT overrides L (a tuning knob).
-constexpr uint64_t kDefaultSplit = 1024;
+// 2048: on the isolated decode, prefix-shared decode and mixed-step
+// benchmarks it measured 1.8% / 1.5% / 2% faster than 1024 keys on one box
+// (fewer workgroup starts and partials); 8 wavefronts per workgroup were
+// slower on the last two.
+constexpr uint64_t kDefaultSplit = 2048;
 
 uint64_t decode_split_keys() {
     const int env = env_int("VO_DECODE_SPLIT", 0);
