@@ -127,8 +127,14 @@ def bench_decode(vo, W, orc, args, cfg):
 
     def step(i):
         layer = i % layers
-        rc = lib.vo_write_kv(wl.pool.handle, layer, kp, vp, S, width, meta_h, stream)
-        rc |= lib.vo_decode_attention(qp, S, heads * hd, wl.pool.handle, layer, meta_h, op, stream)
+        if args.unfused:
+            rc = lib.vo_write_kv(wl.pool.handle, layer, kp, vp, S, width, meta_h, stream)
+            rc |= lib.vo_decode_attention(qp, S, heads * hd, wl.pool.handle, layer, meta_h, op,
+                                          stream)
+        else:
+            # The same two ops as one call (one launch where the step allows it).
+            rc = lib.vo_decode_attention_write_kv(qp, S, heads * hd, kp, vp, width,
+                                                  wl.pool.handle, layer, meta_h, op, stream)
         if rc:
             raise RuntimeError(f"C-ABI call failed: {rc}")
 
@@ -168,7 +174,9 @@ def bench_decode(vo, W, orc, args, cfg):
             "seqs": S, "query_heads": heads, "kv_heads": kvh, "head_dim": hd, "block_size": bs,
             "pool_blocks": cfg["num_blocks"], "context": cfg["ctx_desc"],
             "keys_total": int(wl.row_num_keys().sum()),
-            "step": "write_kv(new tokens) + decode_attention (split-K + reduce)",
+            "step": ("write_kv(new tokens) + decode_attention (split-K + reduce)" +
+                     (", two calls" if args.unfused else
+                      ", one call: vo_decode_attention_write_kv")),
             "layers_rotated": layers,
             "split_keys": int(os.environ.get("VO_DECODE_SPLIT", "2048")),  # the backend's default
         },
@@ -621,6 +629,9 @@ def main():
     ap.add_argument("--model-layers", type=int, default=32,
                     help="cfg4: decoder layers (32 = Llama-3-8B)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--unfused", action="store_true",
+                    help="decode lines: time write_kv and decode_attention as two calls instead "
+                         "of vo_decode_attention_write_kv")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -284,6 +284,22 @@ int32_t vo_step_meta_upload_slots(vo_step_meta *meta, const uint32_t *slots, uin
 int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys, const void *values,
                     uint64_t rows, uint64_t cols, const vo_step_meta *meta, void *stream);
 
+/* write_kv followed by decode_attention on the same decode step
+ * (model.rs:310-316: the step's new keys are cached, then attended), in one
+ * launch where the step allows it: the split-K workgroup holding a row's
+ * last key writes that key's K/V to the pool and uses the new rows directly.
+ * Results (the output and the pool) are bitwise those of vo_write_kv then
+ * vo_decode_attention, which run instead when a slot repeats, rows alias
+ * the block of another row's new slot, the plan packs rows over shared
+ * blocks, or the launch shapes are fixed.  No
+ * counterpart in the reference, whose CPU backend runs the two ops; for
+ * engines that decode with write_kv and decode_attention back to back.
+ * Arguments and errors: those of the two ops. */
+int32_t vo_decode_attention_write_kv(const void *queries, uint64_t rows, uint64_t cols,
+                                     const void *keys, const void *values, uint64_t kv_cols,
+                                     vo_kv_pool *pool, uint64_t layer, const vo_step_meta *meta,
+                                     void *out, void *stream);
+
 /* Backend::prefill_attention (mod.rs:121-135; CPU: cpu/mod.rs:287-312).
  * queries, out: [rows, num_heads * head_dim] bf16 with num_heads = cols /
  * head_dim.  Row t attends to row_num_keys[t] keys of sequence row_seq[t]

@@ -279,6 +279,45 @@ def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, wave
     _assert_close(packed.float().cpu().numpy(), want, f"packed hd={hd} H={heads}")
 
 
+@pytest.mark.parametrize("hd,heads,kvh,shared,fused", [
+    (128, 32, 8, 0, True),     # disjoint tables: one launch
+    (64, 4, 2, 0, True),
+    (128, 16, 1, 640, True),   # blocks shared, none holding a new slot: one launch
+    (128, 32, 8, 640, False),  # shared blocks the plan packs: the two ops
+])
+def test_decode_attention_write_kv_bitwise(vo, hd, heads, kvh, shared, fused):
+    """vo_decode_attention_write_kv equals write_kv then decode_attention,
+    bitwise: the output and the cached new keys.  The new slots hold other
+    values before the call, so the launch must cache the keys itself; the
+    kernel profile shows whether it ran as one launch."""
+    import torch
+    _say(f"decode+write_kv hd={hd} heads={heads} kvh={kvh} shared={shared}")
+    backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=8192,
+                            max_query_heads=heads)
+    ctx = [shared + c for c in EDGE_CTX]
+    wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=16, num_blocks=3000, context_lens=ctx, seed=31 + hd + heads,
+                 shared_prefix=shared, shared_count=len(ctx) if shared else 0)
+    backend.write_kv(wl.pool, 0, wl.k_new, wl.v_new, wl.meta)
+    want = _bits(backend.decode_attention(wl.q, wl.pool, 0, wl.meta))
+    gen = torch.Generator(device="cuda:0").manual_seed(5)
+    junk_k = torch.randn(wl.k_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
+    junk_v = torch.randn(wl.v_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
+    backend.write_kv(wl.pool, 0, junk_k, junk_v, wl.meta)
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    got = backend.decode_attention_write_kv(wl.q, wl.k_new, wl.v_new, wl.pool, 0, wl.meta)
+    torch.cuda.synchronize()
+    vo.enable_profiling(False)
+    kernels = set(vo.profile())
+    assert ("reshape_and_cache" not in kernels) == fused, kernels
+    assert np.array_equal(_bits(got), want)
+    for s_, c in enumerate(ctx):
+        k, v = backend.read_kv(wl.pool, 0, wl.meta, s_, c + 1)
+        assert np.array_equal(_bits(k[c]), _bits(wl.k_new[s_])), f"K of seq {s_}"
+        assert np.array_equal(_bits(v[c]), _bits(wl.v_new[s_])), f"V of seq {s_}"
+
+
 def test_decode_cfg2_full_size(vo, gpu_backend):
     """BASELINE config 2 at full size: 64 seqs, ctx U[512, 4096], 20000-block pool."""
     _say("decode cfg2 full size")

@@ -155,6 +155,8 @@ SIGNATURES = {
     "vo_step_meta_fix_launch": (ctypes.c_int32, [_vp, _u64, _u64, _vp]),
     "vo_step_meta_unfix_launch": (ctypes.c_int32, [_vp]),
     "vo_step_meta_decode_plan": (ctypes.c_int32, [_vp, _vp, _vp, _vp]),
+    "vo_decode_attention_write_kv": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _vp, _u64, _vp, _u64,
+                                                      _vp, _vp, _vp]),
     "vo_embed": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp]),
     "vo_rmsnorm": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp, _vp]),
     "vo_rmsnorm_last_rows": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp,
@@ -789,6 +791,20 @@ class HipBackend:
     def decode_attention(self, queries, pool: KvPool, layer: int, meta: DecodeMeta, out=None,
                          stream=None):
         return self._attention(lib.vo_decode_attention, queries, pool, layer, meta, out, stream)
+
+    def decode_attention_write_kv(self, queries, keys, values, pool: KvPool, layer: int,
+                                  meta: DecodeMeta, out=None, stream=None):
+        """write_kv(keys, values, meta) then decode_attention(queries), as one
+        launch where the step allows it (vo_decode_attention_write_kv)."""
+        import torch
+        m = self._meta_for(pool, meta, stream)
+        if out is None:
+            out = torch.empty_like(queries)
+        _check(lib.vo_decode_attention_write_kv(
+            _dev_ptr(queries), queries.shape[0], queries.shape[1], _dev_ptr(keys),
+            _dev_ptr(values), keys.shape[1], pool.handle, layer, m.handle, _dev_ptr(out),
+            _stream_ptr(stream)))
+        return out
 
     # ---- the rest of the layer (model.rs:269-356) ------------------------
     def embed(self, table, tokens, meta_holder: StepMeta, stream=None):

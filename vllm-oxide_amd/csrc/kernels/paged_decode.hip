@@ -132,6 +132,43 @@ __device__ __forceinline__ void load_chunk(Chunk<HD> &r, const uint16_t *k_head,
     for (int dt = 0; dt < HD / 16; ++dt) r.va[dt] = load_kv<NT>(vp + dt * 16 * kBS);
 }
 
+// The step's new key is chunk key kc of r: take its K and V from the new
+// rows (nk_row, nv_row: this KV head's head_dim values) instead of the pool,
+// which this launch writes them to.  Lane l's K rows are chunk keys
+// 16*(m>=8) + 8*((m>>2)&1) + (m&3) (ka) and that + 4 (kb), m = l%16, dims
+// 8*(l/16) + 32*kk; its V registers hold keys 8*(l/16) .. +7 of dims
+// 16*dt + m (the LaneMap above).
+template <int HD>
+__device__ __forceinline__ void take_new_key(Chunk<HD> &r, uint32_t kc, const uint16_t *nk_row,
+                                             const uint16_t *nv_row, int lane) {
+    const uint32_t m = lane & 15;
+    const uint32_t g = lane >> 4;
+    const uint32_t ka_key = 16 * (m >= 8) + 8 * ((m >> 2) & 1) + (m & 3);
+    if (ka_key == kc) {
+#pragma unroll
+        for (int kk = 0; kk < HD / 32; ++kk)
+            r.ka[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(nk_row + 32 * kk + 8 * g));
+    }
+    if (ka_key + 4 == kc) {
+#pragma unroll
+        for (int kk = 0; kk < HD / 32; ++kk)
+            r.kb[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(nk_row + 32 * kk + 8 * g));
+    }
+    if ((kc >> 3) == g) {
+        const uint32_t i = kc & 7;
+#pragma unroll
+        for (int dt = 0; dt < HD / 16; ++dt) {
+            u32x4 w = __builtin_bit_cast(u32x4, r.va[dt]);
+            const uint32_t val = nv_row[16 * dt + m];
+            const uint32_t sh = 16 * (i & 1);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (q == static_cast<int>(i >> 1)) w[q] = (w[q] & ~(0xffffu << sh)) | (val << sh);
+            r.va[dt] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+}
+
 // Online-softmax update with one chunk.  `nv` = valid keys of this lane's
 // group (0..8); the last chunk of a split passes tail = true.
 template <int HD>
@@ -207,7 +244,9 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                      const uint16_t *__restrict__ q, uint16_t *__restrict__ out,
                      float *__restrict__ part_acc, float *__restrict__ part_ml, uint32_t num_heads,
                      uint32_t group, float scale_log2, const uint32_t *__restrict__ counts,
-                     const uint32_t *__restrict__ mates, uint32_t pack) {
+                     const uint32_t *__restrict__ mates, uint32_t pack, uint16_t *__restrict__ k_w,
+                     uint16_t *__restrict__ v_w, const uint16_t *__restrict__ new_k,
+                     const uint16_t *__restrict__ new_v, const uint32_t *__restrict__ new_slots) {
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
     constexpr uint32_t kTile = kBS * HD;
@@ -238,6 +277,11 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     const uint32_t k_end = min(nk, k_begin + split_keys);
     const uint32_t nblk = (k_end - k_begin + kBS - 1) / kBS;
     const uint32_t nchunks = (k_end - k_begin + kChunk - 1) / kChunk;
+    // With new keys given, the item holding the row's last key caches it
+    // and takes it from new_k / new_v (see NewKeys).
+    const bool take_new = new_k != nullptr && k_end == nk;
+    const uint16_t *nk_row = take_new ? new_k + (static_cast<uint64_t>(row) * kv_heads + kvh) * HD : nullptr;
+    const uint16_t *nv_row = take_new ? new_v + (static_cast<uint64_t>(row) * kv_heads + kvh) * HD : nullptr;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -314,6 +358,8 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     // only they carry the masking code.
     auto run = [&](Chunk<HD> &r, uint32_t cc, bool may_tail) {
         const uint32_t j0 = k_begin + cc * kChunk;
+        if (may_tail && take_new && cc + 1 == nchunks)
+            take_new_key<HD>(r, nk - 1 - j0, nk_row, nv_row, lane);
         const bool tail = may_tail && j0 + kChunk > k_end;
         const int nv = max(0, min(8, static_cast<int>(k_end) - static_cast<int>(j0 + 8 * g)));
         compute_chunk<HD>(r, qv, tail, nv, scale_log2, m_run, l_run, acc);
@@ -338,6 +384,19 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         run(bufB, chunk(k + 1), true);
     } else if (k < mine) {
         run(bufA, chunk(k), true);
+    }
+
+    // Cache the new key (nothing in this launch reads its slot from the pool).
+    if (take_new) {
+        const uint32_t slot = new_slots[row];
+        const uint64_t tile = static_cast<uint64_t>(slot / kBS) * block_stride + static_cast<uint64_t>(kvh) * kTile;
+        const uint32_t t = slot % kBS;
+        for (uint32_t u = threadIdx.x; u < HD / 8; u += 64 * W) {
+            const uint32_t d = 8 * u;
+            *reinterpret_cast<u32x4 *>(k_w + tile + (d / 32) * (kBS * 32) + t * 32 + d % 32) =
+                *reinterpret_cast<const u32x4 *>(nk_row + d);
+        }
+        for (uint32_t d = threadIdx.x; d < HD; d += 64 * W) v_w[tile + d * kBS + t] = nv_row[d];
     }
 
     // The running sums are per lane group; the max is already per head.
@@ -503,7 +562,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
 template <int HD, int W, bool NT>
 hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const DecodePlan &plan,
                         const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
-                        hipStream_t stream) {
+                        hipStream_t stream, const NewKeys *nkeys) {
     const uint32_t group = num_heads / pool.kv_heads;
     const uint32_t pack = plan.pack ? plan.pack : 1;
     if (pack * group > 16 || (pack > 1 && plan.mates == nullptr)) return hipErrorInvalidValue;
@@ -515,19 +574,23 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                        dim3(64 * W), smem, stream, pool.k, pool.v, pool.kv_heads, meta.tables,
                        plan.work, plan.row_info,
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
-                       scale_log2, plan.counts, plan.mates, pack);
+                       scale_log2, plan.counts, plan.mates, pack, pool.k, pool.v,
+                       nkeys ? nkeys->k : nullptr, nkeys ? nkeys->v : nullptr,
+                       nkeys ? nkeys->slots : nullptr);
     return hipGetLastError();
 }
 
 template <int HD>
 hipError_t launch_hd(const PoolLayer &pool, const MetaView &meta, const DecodePlan &plan,
                      const uint16_t *q, uint16_t *out, uint32_t num_heads, float scale_log2,
-                     int waves, hipStream_t stream) {
+                     int waves, hipStream_t stream, const NewKeys *nkeys) {
     hipError_t err;
     const bool nt = plan.streaming;
 #define VO_SPLIT(Wv)                                                                            \
-    (nt ? launch_split<HD, Wv, true>(pool, meta, plan, q, out, num_heads, scale_log2, stream) \
-        : launch_split<HD, Wv, false>(pool, meta, plan, q, out, num_heads, scale_log2, stream))
+    (nt ? launch_split<HD, Wv, true>(pool, meta, plan, q, out, num_heads, scale_log2, stream,  \
+                                     nkeys)                                                  \
+        : launch_split<HD, Wv, false>(pool, meta, plan, q, out, num_heads, scale_log2, stream, \
+                                      nkeys))
     switch (waves) {
         case 1: err = VO_SPLIT(1); break;
         case 2: err = VO_SPLIT(2); break;
@@ -554,18 +617,21 @@ bool decode_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t grou
 hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               const DecodePlan &plan, const uint16_t *q, uint16_t *out,
                               uint32_t num_heads, float scale, int waves_per_group,
-                              hipStream_t stream) {
+                              hipStream_t stream, const NewKeys *new_keys) {
     if (plan.launch_work == 0) return hipSuccess;
+    // New keys need one item per row holding its last key: not with packing
+    // (the launcher's caller plans without it) nor a fixed launch.
+    if (new_keys && (plan.pack > 1 || plan.launch_work != plan.num_work)) return hipErrorInvalidValue;
     if (plan.split_keys == 0 || plan.split_keys % kChunk != 0 || plan.split_keys > kMaxSplitKeys)
         return hipErrorInvalidValue;
     const float scale_log2 = scale * 1.4426950408889634f;
     switch (pool.head_dim) {
         case 64:
             return launch_hd<64>(pool, meta, plan, q, out, num_heads, scale_log2, waves_per_group,
-                                 stream);
+                                 stream, new_keys);
         case 128:
             return launch_hd<128>(pool, meta, plan, q, out, num_heads, scale_log2,
-                                  waves_per_group, stream);
+                                  waves_per_group, stream, new_keys);
         default:
             return hipErrorInvalidValue;
     }

@@ -180,10 +180,22 @@ bool decode_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t grou
 
 // MFMA split-K decode (one launch) and, when a row has several splits, the
 // reduce kernel (a second launch).
+// The step's new keys, for a decode launch that also caches them (the
+// write_kv before decode_attention, in the same launch): the item holding a
+// row's last key writes row r of k and v ([rows][kv_heads * head_dim] bf16)
+// to the pool at slots[r] and takes that key's K/V from k and v instead of
+// the pool.  The caller guarantees that no slot repeats and that no other
+// row of the step reads a block these slots are in.
+struct NewKeys {
+    const uint16_t *k;
+    const uint16_t *v;
+    const uint32_t *slots;  // [rows]
+};
+
 hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               const DecodePlan &plan, const uint16_t *q, uint16_t *out,
                               uint32_t num_heads, float scale, int waves_per_group,
-                              hipStream_t stream);
+                              hipStream_t stream, const NewKeys *new_keys = nullptr);
 
 // Work plan of the MFMA prefill kernel: one item per 32-row query tile of a
 // sequence, longest first.

@@ -266,6 +266,7 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
         }
         for (uint64_t r = 0; r < num_rows; ++r)
             h[r] = (!dup || last[slot_mapping[r]] == r) ? slot_mapping[r] : kSkipSlot;
+        m->slots_repeat = dup;
     }
     m->d_write_slots = dp;
     m->view.slot_mapping = dp;
@@ -516,6 +517,30 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
         m->plan.launch_reduce = static_cast<uint32_t>(nred);
     }
     m->decode_planned = true;
+    // New keys cached by the decode launch: a whole decode step without
+    // repeated slots, no packing and no fixed launch, and no block holding a
+    // new slot read by another sequence (with a streaming plan no block is
+    // shared at all).
+    m->fused_write_ok = false;
+    if (!rows && !pk.fixed() && P == 1 && !m->slots_repeat && m->kind == kDecode) {
+        bool ok = true;
+        if (!streaming) {
+            const uint64_t bs = m->block_size;
+            m->seq_keys.assign(m->num_seqs, 0);
+            for (uint64_t r = 0; r < T; ++r)
+                m->seq_keys[m->row_seq[r]] =
+                    std::max<uint64_t>(m->seq_keys[m->row_seq[r]], m->row_num_keys[r]);
+            m->block_seen.assign(static_cast<size_t>(m->max_block) + 1, 0);  // readers, up to 2
+            for (uint64_t seq = 0; seq < m->num_seqs; ++seq) {
+                const uint64_t used = (m->seq_keys[seq] + bs - 1) / bs;
+                const uint32_t *t = m->tables.data() + m->table_off[seq];
+                for (uint64_t i = 0; i < used; ++i)
+                    if (m->block_seen[t[i]] < 2) ++m->block_seen[t[i]];
+            }
+            for (uint64_t r = 0; r < T && ok; ++r) ok = m->block_seen[m->slots[r] / bs] < 2;
+        }
+        m->fused_write_ok = ok;
+    }
     return VO_OK;
 }
 
@@ -1329,6 +1354,45 @@ extern "C" int32_t vo_decode_attention(const void *queries, uint64_t rows, uint6
             static_cast<uint16_t *>(out), heads, scale, static_cast<hipStream_t>(stream));
     }
     return device_status(op, err);
+}
+
+extern "C" int32_t vo_decode_attention_write_kv(const void *queries, uint64_t rows,
+                                                uint64_t cols, const void *keys,
+                                                const void *values, uint64_t kv_cols,
+                                                vo_kv_pool *pool, uint64_t layer,
+                                                const vo_step_meta *m, void *out, void *stream) {
+    const char *op = "decode_attention_write_kv";
+    if (!pool || !m) return fail_argument(op, "null pool or meta");
+    if (vo_status rc = check_write(pool, layer, rows, kv_cols, m)) return rc;
+    if (vo_status rc = check_attention(op, queries, rows, cols, pool, layer, m, out, kDecode))
+        return rc;
+    if (rows == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!keys || !values) return fail_argument(op, "null keys or values");
+    if (!aligned16(keys) || !aligned16(values))
+        return fail_argument(op, "keys and values must be 16-byte aligned");
+    const vo_kv_layout &L = pool->layout;
+    const uint32_t heads = static_cast<uint32_t>(cols / L.head_dim);
+    const uint32_t group = heads / static_cast<uint32_t>(L.kv_heads);
+    if (m->fused_write_ok && m->decode_planned &&
+        kernels::decode_mfma_supported(static_cast<uint32_t>(L.head_dim),
+                                       static_cast<uint32_t>(L.block_size), group)) {
+        DeviceGuard guard(pool->device);
+        const float scale = 1.0f / std::sqrt(static_cast<float>(L.head_dim));  // attention.rs:88
+        const kernels::NewKeys nk{static_cast<const uint16_t *>(keys),
+                                  static_cast<const uint16_t *>(values), m->d_write_slots};
+        const hipError_t err = kernels::launch_decode_mfma(
+            pool->layer(layer), m->view, m->plan, static_cast<const uint16_t *>(queries),
+            static_cast<uint16_t *>(out), heads, scale, decode_waves(),
+            static_cast<hipStream_t>(stream), &nk);
+        return device_status(op, err);
+    }
+    // Otherwise the two ops in sequence, with the same results.
+    if (const int32_t rc = vo_write_kv(pool, layer, keys, values, rows, kv_cols, m, stream))
+        return rc;
+    return vo_decode_attention(queries, rows, cols, pool, layer, m, out, stream);
 }
 
 extern "C" int32_t vo_prefill_meta_build_device(

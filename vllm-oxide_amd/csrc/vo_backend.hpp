@@ -169,6 +169,11 @@ struct vo_step_meta {
     vo::kernels::WritePlan write_plan{};      // runs of consecutive slots inside one block
     vo::kernels::DecodePlan plan{};
     bool decode_planned = false;
+    bool slots_repeat = false;  // a slot appears in two rows of the step
+    // Decode step whose new keys can be cached by the decode launch itself
+    // (vo_decode_attention_write_kv): no slot repeats and no row reads a
+    // block holding another row's new slot.
+    bool fused_write_ok = false;
     std::vector<vo::TailItem> tail_items;  // scratch of plan_decode (capacity kept across steps)
     std::vector<uint8_t> block_seen;   // scratch of plan_decode: one byte per physical block
     std::vector<uint64_t> seq_keys;    // scratch of plan_decode: keys read per sequence
