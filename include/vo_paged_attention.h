@@ -290,8 +290,7 @@ int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys, const vo
  * last key writes that key's K/V to the pool and uses the new rows directly.
  * Results (the output and the pool) are bitwise those of vo_write_kv then
  * vo_decode_attention, which run instead when a slot repeats, rows alias
- * the block of another row's new slot, the plan packs rows over shared
- * blocks, or the launch shapes are fixed.  No
+ * the block of another row's new slot, or the launch shapes are fixed.  No
  * counterpart in the reference, whose CPU backend runs the two ops; for
  * engines that decode with write_kv and decode_attention back to back.
  * Arguments and errors: those of the two ops. */

@@ -279,13 +279,14 @@ def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, wave
     _assert_close(packed.float().cpu().numpy(), want, f"packed hd={hd} H={heads}")
 
 
-@pytest.mark.parametrize("hd,heads,kvh,shared,fused", [
-    (128, 32, 8, 0, True),     # disjoint tables: one launch
-    (64, 4, 2, 0, True),
-    (128, 16, 1, 640, True),   # blocks shared, none holding a new slot: one launch
-    (128, 32, 8, 640, False),  # shared blocks the plan packs: the two ops
+@pytest.mark.parametrize("hd,heads,kvh,shared,fixed", [
+    (128, 32, 8, 0, False),     # disjoint tables: one launch
+    (64, 4, 2, 0, False),
+    (128, 16, 1, 640, False),   # blocks shared, none holding a new slot: one launch
+    (128, 32, 8, 2048, False),  # shared blocks that the plan packs: one launch
+    (128, 32, 8, 0, True),      # fixed launch shapes: the two ops
 ])
-def test_decode_attention_write_kv_bitwise(vo, hd, heads, kvh, shared, fused):
+def test_decode_attention_write_kv_bitwise(vo, hd, heads, kvh, shared, fixed):
     """vo_decode_attention_write_kv equals write_kv then decode_attention,
     bitwise: the output and the cached new keys.  The new slots hold other
     values before the call, so the launch must cache the keys itself; the
@@ -304,18 +305,25 @@ def test_decode_attention_write_kv_bitwise(vo, hd, heads, kvh, shared, fused):
     junk_k = torch.randn(wl.k_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
     junk_v = torch.randn(wl.v_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
     backend.write_kv(wl.pool, 0, junk_k, junk_v, wl.meta)
+    if fixed:
+        backend.step_meta(wl.pool).fix_launch(len(ctx), 0)
+    else:
+        work, parts, _ = backend.step_meta(wl.pool).decode_plan()
+        assert (work < parts) == (shared >= 2048), (work, parts)  # packed items over the prefix
     vo.profile_reset()
     vo.enable_profiling(True)
     got = backend.decode_attention_write_kv(wl.q, wl.k_new, wl.v_new, wl.pool, 0, wl.meta)
     torch.cuda.synchronize()
     vo.enable_profiling(False)
     kernels = set(vo.profile())
-    assert ("reshape_and_cache" not in kernels) == fused, kernels
+    assert ("reshape_and_cache" in kernels) == fixed, kernels
     assert np.array_equal(_bits(got), want)
     for s_, c in enumerate(ctx):
         k, v = backend.read_kv(wl.pool, 0, wl.meta, s_, c + 1)
         assert np.array_equal(_bits(k[c]), _bits(wl.k_new[s_])), f"K of seq {s_}"
         assert np.array_equal(_bits(v[c]), _bits(wl.v_new[s_])), f"V of seq {s_}"
+    if fixed:
+        backend.step_meta(wl.pool).unfix_launch()
 
 
 def test_decode_cfg2_full_size(vo, gpu_backend):

@@ -619,9 +619,8 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               uint32_t num_heads, float scale, int waves_per_group,
                               hipStream_t stream, const NewKeys *new_keys) {
     if (plan.launch_work == 0) return hipSuccess;
-    // New keys need one item per row holding its last key: not with packing
-    // (the launcher's caller plans without it) nor a fixed launch.
-    if (new_keys && (plan.pack > 1 || plan.launch_work != plan.num_work)) return hipErrorInvalidValue;
+    // New keys need exactly the plan's items (not a fixed launch's grid).
+    if (new_keys && plan.launch_work != plan.num_work) return hipErrorInvalidValue;
     if (plan.split_keys == 0 || plan.split_keys % kChunk != 0 || plan.split_keys > kMaxSplitKeys)
         return hipErrorInvalidValue;
     const float scale_log2 = scale * 1.4426950408889634f;

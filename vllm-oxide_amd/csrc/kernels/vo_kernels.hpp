@@ -185,7 +185,8 @@ bool decode_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t grou
 // row's last key writes row r of k and v ([rows][kv_heads * head_dim] bf16)
 // to the pool at slots[r] and takes that key's K/V from k and v instead of
 // the pool.  The caller guarantees that no slot repeats and that no other
-// row of the step reads a block these slots are in.
+// row of the step reads a block these slots are in (so a packed item, whose
+// blocks several rows read, holds no row's last key).
 struct NewKeys {
     const uint16_t *k;
     const uint16_t *v;

@@ -518,11 +518,12 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     }
     m->decode_planned = true;
     // New keys cached by the decode launch: a whole decode step without
-    // repeated slots, no packing and no fixed launch, and no block holding a
-    // new slot read by another sequence (with a streaming plan no block is
-    // shared at all).
+    // repeated slots or a fixed launch, and no block holding a new slot read
+    // by another sequence (with a streaming plan no block is shared at all).
+    // A packed item's blocks are read by several rows, so under these
+    // conditions it never holds a row's last key.
     m->fused_write_ok = false;
-    if (!rows && !pk.fixed() && P == 1 && !m->slots_repeat && m->kind == kDecode) {
+    if (!rows && !pk.fixed() && !m->slots_repeat && m->kind == kDecode) {
         bool ok = true;
         if (!streaming) {
             const uint64_t bs = m->block_size;
