@@ -18,8 +18,12 @@ out rows, and the block-table entries.  tokens_per_s = 64 / step time.
 roofline.achieved = the same bytes / the split-K kernel's average duration,
 timed live with HIP events around each launch.
 
---config cfg3 / cfg5 print an extra line for the prefill and prefix-shared
-decode configs.
+The default run prints that cfg2 line with two nested records for the
+north_star's other targets, each with its own roofline and CPU baseline:
+"cfg5" (prefix-shared decode at the Llama-3-70B layer shape, HBM roofline on
+the unique bytes) and "cfg3" (chunked prefill, bf16 MFMA roofline on the
+causal-aware FLOPs).  --config cfg3 / cfg5 / cfg4 / cfg4a print one config's
+full line instead; --headline-only drops the nested records.
 """
 import argparse
 import ctypes
@@ -60,6 +64,24 @@ def cpu_info():
     except AttributeError:
         avail = os.cpu_count() or 1
     return model, avail
+
+
+def cpu_threads(rows, args):
+    """Threads for the CPU baseline: every CPU this process may run on (its
+    affinity), within the job's CPU share when the environment states one
+    (OMP_NUM_THREADS: the GPU box allots 16 CPUs to a one-GPU job and sets it
+    to 16), and at most one per row (the reference's CPU attention is parallel
+    over rows only, attention.rs:54-71, rayon's default pool).  Returns (used,
+    available by affinity, share or None)."""
+    _, avail = cpu_info()
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "") or 0) or None
+    except ValueError:
+        share = None
+    n = avail if share is None else min(avail, share)
+    if args.cpu_threads:
+        n = min(n, args.cpu_threads)
+    return max(1, min(n, rows)), avail, share
 
 
 def profile_record(kernel, workload):
@@ -181,7 +203,10 @@ def bench_decode(vo, W, orc, args, cfg):
             "split_keys": int(os.environ.get("VO_DECODE_SPLIT", "2048")),  # the backend's default
         },
         "tokens_per_s": round(S / sec, 1),
-        "pct_of_hbm_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
+        # HBM bytes move once per physical block, so the fraction of peak is
+        # taken on the unique bytes (equal to the algorithmic bytes when no
+        # block is shared, as in cfg2).
+        "pct_of_hbm_peak": round(100.0 * ubytes / sec / 1e9 / HBM_PEAK_GBS, 2),
         "algorithmic_bytes_per_step": nbytes,
         "unique_bytes_per_step": ubytes,
         "kernels_us": {k: round(v["avg_ms"] * 1e3, 2) for k, v in prof.items()},
@@ -207,8 +232,8 @@ def cpu_baseline(orc, W, wl, nbytes, args):
     """The oracle (C restatement of the reference's CPU attention, row-parallel
     like rayon) on the same workload: the whole decode_attention of the step,
     repeated until about args.cpu_seconds have passed."""
-    model, avail = cpu_info()
-    threads = min(avail, args.cpu_threads)
+    model, _ = cpu_info()
+    threads, avail, share = cpu_threads(wl.rows, args)
     pool = W.oracle_pool(orc, wl)
     times = []
     t_end = time.perf_counter() + args.cpu_seconds
@@ -230,6 +255,8 @@ def cpu_baseline(orc, W, wl, nbytes, args):
         "ms_per_step": round(med * 1e3, 2),
         "single_thread_ms_per_step": round(single * 1e3, 2),
         "cores": threads,
+        "cores_available": avail,
+        "cpu_share": share,
         "kind": "port",
         "cpu": model,
         "sample": (f"full decode_attention of the same step ({S} rows, f32 oracle on the bf16 "
@@ -245,8 +272,8 @@ def cpu_baseline_model(orc, W, cfg, ctx, new, args):
     is 1536) -- with f32 weights ~ N(0, 0.02), plus the LM head for 8 rows.
     Scaled linearly to the step: 32 layers x 1280 rows and 258 LM-head rows
     (the GEMMs, 94% of the reference's CPU time, scale with rows)."""
-    model_name, avail = cpu_info()
-    threads = min(avail, args.cpu_threads)
+    model_name, _ = cpu_info()
+    threads, avail, share = cpu_threads(32, args)
     rng = np.random.default_rng(14)
     H, F, V, hd = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.head_dim
     KVH, NH = cfg.num_key_value_heads, cfg.num_attention_heads
@@ -307,7 +334,8 @@ def cpu_baseline_model(orc, W, cfg, ctx, new, args):
     t_head = time.perf_counter() - t0
     step = cfg.num_hidden_layers * t_layer * (1280 / rows) + t_head * (258 / 8)
     return {
-        "value": round(1280 / step, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "value": round(1280 / step, 2), "unit": "tokens/s", "cores": threads,
+        "cores_available": avail, "cpu_share": share, "kind": "port",
         "cpu": model_name, "est_ms_per_step": round(step * 1e3, 1),
         "sample": (f"one decoder layer for {rows} of the step's 1280 rows (8 decode rows with "
                    f"their contexts, 24 rows of the 1536-context chunk) and the LM head for 8 "
@@ -324,7 +352,7 @@ def bench_prefill(vo, W, orc, args):
                             max_query_heads=heads)
     wl = W.build(vo, backend, kind="prefill", heads=heads, kv_heads=kvh, head_dim=hd,
                  block_size=bs, num_blocks=12000, context_lens=ctx, num_new=[512] * 8, seed=3,
-                 keep_host=False)
+                 keep_host=not args.no_cpu)
     out = torch.empty_like(wl.q)
 
     def step(i):
@@ -356,6 +384,38 @@ def bench_prefill(vo, W, orc, args):
                      # Cycles the MFMA pipe was busy / all cycles, from the
                      # committed counter record (SQ_VALU_MFMA_BUSY_CYCLES).
                      "mfma_busy": rec.get("mfma_busy_frac")},
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_prefill(orc, W, wl, args),
+    }
+
+
+def cpu_baseline_prefill(orc, W, wl, args):
+    """The oracle's prefill_attention (the reference's CPU attention restated
+    in C, row-parallel) on a bounded sample of the cfg3 step: every 8th row of
+    the 4096 (512 rows, the same positions in every sequence), repeated for
+    about args.cpu_seconds.  Reported as causal-aware TFLOP/s of the sampled
+    rows, the unit of the GPU figure; the whole step would take 8x as long."""
+    model, _ = cpu_info()
+    rows = np.arange(0, wl.rows, 8)
+    threads, avail, share = cpu_threads(len(rows), args)
+    pool = W.oracle_pool(orc, wl)
+    flops = int(wl.row_num_keys()[rows].sum()) * wl.heads * 4 * wl.head_dim
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    while True:
+        t0 = time.perf_counter()
+        W.oracle_attention(orc, wl, pool=pool, rows=rows, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end or len(times) >= 200:
+            break
+    med = float(np.median(times))
+    return {
+        "value": round(flops / med / 1e12, 4), "unit": "TFLOP/s",
+        "est_ms_per_step": round(med * 1e3 * wl.rows / len(rows), 1),
+        "cores": threads, "cores_available": avail, "cpu_share": share, "kind": "port",
+        "cpu": model,
+        "sample": (f"prefill_attention of {len(rows)} of the step's {wl.rows} rows (every 8th, "
+                   f"f32 oracle on the bf16 inputs), median of {len(times)} runs; causal-aware "
+                   f"FLOPs of those rows; est_ms_per_step scales by rows"),
     }
 
 
@@ -614,6 +674,16 @@ def bench_rope_write(vo, W, orc, args):
                                    "theta 500000 llama3 scaling", "shapes": res}}
 
 
+def nested_record(line):
+    """The fields of a config's own line that the headline line nests."""
+    keep = ("metric", "value", "unit", "ms_per_step", "pct_of_hbm_peak", "tokens_per_s",
+            "kernels_us", "roofline", "cpu_baseline", "algorithmic_bytes_per_step",
+            "unique_bytes_per_step")
+    out = {k: line[k] for k in keep if k in line}
+    out["workload"] = line["config"]["workload"]
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -633,7 +703,11 @@ def main():
                     help="decode lines: time write_kv and decode_attention as two calls instead "
                          "of vo_decode_attention_write_kv")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="cap on the CPU baseline's threads (0: every CPU of the job's share)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="default config: print the cfg2 line without the nested cfg3 and cfg5 "
+                         "records")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (scales the HBM byte "
                          "counters of rocprofv3 --pmc)")
@@ -663,19 +737,26 @@ def main():
     import oracle as orc
     import workloads as W
 
+    cfg2 = dict(name="cfg2: isolated paged decode, Llama-3-8B shape", heads=32,
+                ctx=W.cfg2_context_lens(), seed=2, num_blocks=20000,
+                ctx_desc="U[512, 4096], seed 2, keys = ctx + 1")
+    cfg5 = dict(name="cfg5: prefix-shared decode, Llama-3-70B layer shape", heads=64,
+                ctx=W.cfg5_context_lens(), seed=5, num_blocks=40000, shared_prefix=4096,
+                shared_count=64,
+                ctx_desc="64 x (4096 shared + U[256,1024]) + 1 x 32768, seed 5",
+                metric="prefix-shared decode attn GB/s (logical bytes), Llama-3-70B layer")
     lines = []
-    if args.config in ("cfg2", "all"):
-        cfg = dict(name="cfg2: isolated paged decode, Llama-3-8B shape", heads=32,
-                   ctx=W.cfg2_context_lens(), seed=2, num_blocks=20000,
-                   ctx_desc="U[512, 4096], seed 2, keys = ctx + 1")
-        lines.append(bench_decode(vo, W, orc, args, cfg))
+    if args.config == "cfg2" and not args.headline_only:
+        # The headline (cfg2) line, with the other two north_star targets
+        # nested: cfg5's prefix-shared decode and cfg3's chunked prefill.
+        line = bench_decode(vo, W, orc, args, cfg2)
+        line["cfg5"] = nested_record(bench_decode(vo, W, orc, args, cfg5))
+        line["cfg3"] = nested_record(bench_prefill(vo, W, orc, args))
+        lines.append(line)
+    elif args.config in ("cfg2", "all"):
+        lines.append(bench_decode(vo, W, orc, args, cfg2))
     if args.config in ("cfg5", "all"):
-        cfg = dict(name="cfg5: prefix-shared decode, Llama-3-70B layer shape", heads=64,
-                   ctx=W.cfg5_context_lens(), seed=5, num_blocks=40000, shared_prefix=4096,
-                   shared_count=64,
-                   ctx_desc="64 x (4096 shared + U[256,1024]) + 1 x 32768, seed 5",
-                   metric="prefix-shared decode attn GB/s (logical bytes), Llama-3-70B layer")
-        lines.append(bench_decode(vo, W, orc, args, cfg))
+        lines.append(bench_decode(vo, W, orc, args, cfg5))
     if args.config in ("cfg3", "all"):
         lines.append(bench_prefill(vo, W, orc, args))
     if args.config in ("cfg4a", "all"):

@@ -13,7 +13,12 @@
  *   Backend::write_kv        (mod.rs:107-119) -> vo_write_kv
  *   Backend::prefill_attention (mod.rs:121-135) -> vo_prefill_attention
  *   Backend::decode_attention  (mod.rs:137-149) -> vo_decode_attention
- *   Backend::read            (mod.rs:177-181) -> vo_gather_kv (debug/test only)
+ *   Backend::read            (mod.rs:177-181) -> vo_workspace_read; vo_gather_kv
+ *                                                  reads the pool (both debug/test only)
+ *   Backend::alloc_workspace (mod.rs:76-77)   -> vo_workspace_create
+ *   Backend::workspace_elems (mod.rs:78)      -> vo_workspace_elems
+ *   Backend::upload          (mod.rs:69-70)   -> vo_weight_upload
+ *   Backend::weight_shape    (mod.rs:71-72)   -> vo_weight_shape
  *
  * plus the paged-KV addressing of crates/engine/src/backend/paged.rs
  * (slot_of, PrefillMeta::new, DecodeMeta::new, last_rows) as host functions,
@@ -67,8 +72,12 @@ typedef enum vo_status {
     VO_ERR_INVALID_ARGUMENT = 7,       /* NULL pointer or zero size where one is required */
     VO_ERR_UNSUPPORTED = 8,            /* shape outside what the kernels are built for */
     VO_ERR_POSITION_OUT_OF_RANGE = 9,  /* EngineError::PositionOutOfRange error.rs:52-53 */
-    VO_ERR_NAN = 10                    /* EngineError::NaN              error.rs:54-55 */
+    VO_ERR_NAN = 10,                   /* EngineError::NaN              error.rs:54-55 */
+    VO_ERR_OUTSIDE_WORKSPACE = 11      /* EngineError::OutsideWorkspace error.rs:47-48 */
 } vo_status;
+
+/* Element type of an activation buffer or a weight. */
+typedef enum vo_dtype { VO_DTYPE_BF16 = 0, VO_DTYPE_F32 = 1 } vo_dtype;
 
 /* Detail of the last failed call on the calling thread.  The numeric fields
  * carry what the reference's error variant carries:
@@ -95,6 +104,59 @@ typedef struct vo_error_info {
 int32_t vo_last_error(vo_error_info *out);
 const char *vo_status_name(int32_t status);
 const char *vo_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Device memory the engine gets from the backend (mod.rs:61-78)       */
+/* ------------------------------------------------------------------ */
+
+/* Opaque.  The activation workspace (Backend::alloc_workspace, mod.rs:76-77):
+ * one device allocation of `elems` 4-byte elements, zero-filled (the
+ * reference's f32 workspace, cpu/mod.rs:163-166), allocated once at startup.
+ * The engine's arena carves it into Regions {offset, rows, cols} in elements
+ * (mod.rs:31-38); vo_workspace_region turns one into the device address the
+ * ops take.  A Region's address is base + 4 * offset whatever the element type
+ * the op keeps there: the ops on this path read and write bf16 activations
+ * (2 bytes per value, so such a region uses the first half of its bytes) and
+ * f32 for the residual stream and the logits. */
+typedef struct vo_workspace vo_workspace;
+
+int32_t vo_workspace_create(int32_t device, uint64_t elems, vo_workspace **out);
+void vo_workspace_destroy(vo_workspace *ws);
+/* Backend::workspace_elems (mod.rs:78); 0 for NULL. */
+uint64_t vo_workspace_elems(const vo_workspace *ws);
+/* Device address of Region {offset, rows, cols}.  VO_ERR_OUTSIDE_WORKSPACE
+ * when offset + rows * cols > elems (cpu/mod.rs:57-62). */
+int32_t vo_workspace_region(const vo_workspace *ws, uint64_t offset, uint64_t rows, uint64_t cols,
+                            void **ptr);
+/* Backend::read (mod.rs:177-181): the Region's rows * cols values of `dtype`
+ * (VO_DTYPE_BF16 widened exactly, or VO_DTYPE_F32) into host_out as f32.
+ * Waits for `stream` first; debug and tests only, never in the hot loop.
+ * VO_ERR_OUTSIDE_WORKSPACE as vo_workspace_region. */
+int32_t vo_workspace_read(const vo_workspace *ws, uint64_t offset, uint64_t rows, uint64_t cols,
+                          int32_t dtype, float *host_out, void *stream);
+
+/* Opaque.  A weight resident on one device (Backend::Weight, mod.rs:64-66). */
+typedef struct vo_weight vo_weight;
+
+/* Backend::upload (mod.rs:69-70): the host Weight (weights.rs:20-24: f32,
+ * row-major, matrices [out_features, in_features]) of `ndim` dimensions
+ * `shape` to `device`, as bf16 (VO_DTYPE_BF16: rounded to nearest even; what
+ * the ops take) or f32.  Synchronous: `data` may be freed on return. */
+int32_t vo_weight_upload(int32_t device, const float *data, const uint64_t *shape, uint64_t ndim,
+                         int32_t dtype, vo_weight **out);
+/* One weight holding `count` uploaded matrices of the same dtype, device and
+ * column count, stacked by rows (a device copy).  No counterpart in the
+ * reference, whose Llama::new uploads q/k/v and gate/up one by one
+ * (model.rs:157-165): stacked, each group is one GEMM over the same input
+ * (vo_qkv_rope_write_kv reads the [q | k | v] rows of such a product). */
+int32_t vo_weight_concat_rows(const vo_weight *const *parts, uint64_t count, vo_weight **out);
+void vo_weight_destroy(vo_weight *w);
+/* Backend::weight_shape (mod.rs:71-72): *ndim dimensions, the first
+ * `capacity` of them into shape (shape may be NULL to ask for ndim). */
+int32_t vo_weight_shape(const vo_weight *w, uint64_t *shape, uint64_t capacity, uint64_t *ndim);
+/* The device address and element type (vo_dtype) the ops take. */
+const void *vo_weight_data(const vo_weight *w);
+int32_t vo_weight_dtype(const vo_weight *w);
 
 /* ------------------------------------------------------------------ */
 /* Paged-KV addressing, host side (paged.rs)                          */
@@ -448,9 +510,6 @@ int32_t vo_rope_write_kv(vo_kv_pool *pool, uint64_t layer, const vo_rope_table *
 /* ------------------------------------------------------------------ */
 /* The rest of the layer (Llama::forward, model.rs:269-356)            */
 /* ------------------------------------------------------------------ */
-
-/* Element type of an activation buffer. */
-typedef enum vo_dtype { VO_DTYPE_BF16 = 0, VO_DTYPE_F32 = 1 } vo_dtype;
 
 /* The step's token ids (Llama::prefill / decode `tokens`, model.rs:221-243),
  * kept apart from the attention metadata: a host copy for embed's check and

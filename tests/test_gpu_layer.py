@@ -403,6 +403,93 @@ def test_cfg1_free_running_greedy_matches_until_a_near_tie(vo, M, gpu_backend):
             f"seq {s} diverges at id {i} where the oracle's gap is {gap:.3e}")
 
 
+# Config 1 as BASELINE states it: the oracle runs the f32 N(0, 0.02) weights,
+# the GPU holds them rounded to bf16.  On the CPU, the oracle on bf16-rounded
+# weights differs from the oracle on the f32 ones by at most 0.0065 in the
+# logits over prefill + 32 steps (0.55 of LOGIT_ATOL + LOGIT_RTOL * |x|, seeds
+# 1 and 2), and the GPU's bf16 activations add at most 0.55 of it against
+# the oracle on bf16 weights; the sum stays within twice that tolerance.
+F32W_ATOL, F32W_RTOL = 2 * LOGIT_ATOL, 2 * LOGIT_RTOL
+
+
+def test_cfg1_f32_weights_logits_and_gap_aware_greedy(vo, M, gpu_backend):
+    """BASELINE config 1 with its f32 weights on the oracle side.  Teacher
+    forced: every step's logits within F32W_ATOL + F32W_RTOL * |oracle| and the
+    ids equal wherever the oracle's top-1 / top-2 gap exceeds twice that.
+    Free running (hf_match.rs:139-155): per sequence the first id that differs,
+    if any, sits where the oracle's gap is within the tolerance."""
+    cfg = W.cfg1_config()
+    w32 = W.normal_weights(cfg, 101)
+    rng = np.random.default_rng(1)
+    lens = [17, 33, 64, 100]
+    prompts = [list(map(int, rng.integers(0, cfg.vocab_size, n))) for n in lens]
+    steps = 32
+    tables = [list(map(int, t)) for t in
+              W.split_tables(rng, [-(-(n + steps) // 16) for n in lens], 64)]
+    seqs0 = [(0, n, t) for n, t in zip(lens, tables)]
+    om = orc.Llama(cfg, w32, num_blocks=64, block_size=16, max_len=256)
+    ids, want = om.prefill(sum(prompts, []), seqs0, 16)
+    want_ids, want_logits = [list(map(int, ids))], [want]
+    ctx = list(lens)
+    for _ in range(steps):
+        ids, lg = om.decode(want_ids[-1], [(c, t) for c, t in zip(ctx, tables)], 16)
+        want_ids.append(list(map(int, ids)))
+        want_logits.append(lg)
+        ctx = [c + 1 for c in ctx]
+    want_ids = np.array(want_ids)
+
+    def tol(x):
+        return F32W_ATOL + F32W_RTOL * np.abs(x)
+
+    _say("cfg1 f32 weights: teacher forced")
+    gm, kv = _gpu_model(vo, M, gpu_backend, cfg, w32, 64, 16)  # rounds to bf16 on upload
+    got = gm.prefill(kv, sum(prompts, []), vo.PrefillMeta.new(
+        [vo.PrefillSeq(*s) for s in seqs0], 16), True)
+    worst_abs, worst_rel, checked, near = 0.0, 0.0, 0, 0
+    ctx = list(lens)
+    for step in range(steps + 1):
+        want = want_logits[step]
+        err = np.abs(got.logits - want)
+        worst_abs = max(worst_abs, float(err.max()))
+        worst_rel = max(worst_rel, float((err / tol(want)).max()))
+        assert (err <= tol(want)).all(), f"step {step}: max logit err {err.max():.3e}"
+        top2 = np.sort(want, axis=1)[:, -2:]
+        for s in range(4):
+            if top2[s, 1] - top2[s, 0] > 2 * tol(top2[s, 1]):
+                assert got.tokens[s] == want_ids[step][s], f"step {step} seq {s}"
+                checked += 1
+            else:
+                near += 1
+        if step == steps:
+            break
+        got = gm.decode(kv, list(want_ids[step]), vo.DecodeMeta.new(
+            [vo.DecodeSeq(c, t) for c, t in zip(ctx, tables)], 16), True)
+        ctx = [c + 1 for c in ctx]
+    _say(f"cfg1 f32 weights: worst |dlogit| {worst_abs:.3e} ({worst_rel:.3f} of the tolerance); "
+         f"ids checked {checked}, near-ties {near}")
+
+    _say("cfg1 f32 weights: free running")
+    gm, kv = _gpu_model(vo, M, gpu_backend, cfg, w32, 64, 16)
+    o = gm.prefill(kv, sum(prompts, []), vo.PrefillMeta.new([vo.PrefillSeq(*s) for s in seqs0], 16))
+    gen, ctx = [o.tokens], list(lens)
+    for _ in range(steps):
+        o = gm.decode(kv, gen[-1], vo.DecodeMeta.new(
+            [vo.DecodeSeq(c, t) for c, t in zip(ctx, tables)], 16))
+        gen.append(o.tokens)
+        ctx = [c + 1 for c in ctx]
+    gen = np.array(gen)
+    for s in range(4):
+        diff = np.nonzero(gen[:, s] != want_ids[:, s])[0]
+        if len(diff) == 0:
+            _say(f"cfg1 f32 weights seq {s}: all {steps + 1} ids equal")
+            continue
+        i = int(diff[0])
+        top2 = np.sort(want_logits[i][s])[-2:]
+        gap = float(top2[1] - top2[0])
+        _say(f"cfg1 f32 weights seq {s}: first difference at id {i}, oracle gap {gap:.3e}")
+        assert gap <= 2 * tol(top2[1]), f"seq {s} diverges at id {i} where the gap is {gap:.3e}"
+
+
 def test_cfg1_mixed_step_matches_oracle(vo, M, gpu_backend):
     """A continuous-batching step: two sequences decode one token while a
     third prefills a 40-token chunk onto 24 cached tokens, one prefill call

@@ -326,6 +326,77 @@ def test_decode_attention_write_kv_bitwise(vo, hd, heads, kvh, shared, fixed):
         backend.step_meta(wl.pool).unfix_launch()
 
 
+@pytest.mark.parametrize("case", ["two_rows_one_seq", "slot_not_last_key", "zero_keys",
+                                  "tail_block_shared", "repeated_slot"])
+def test_decode_attention_write_kv_noncanonical_falls_back(vo, case):
+    """vo_decode_attention_write_kv on decode metadata that DecodeMeta::new
+    would not build (its fields are public, paged.rs:173-186): two rows of one
+    sequence, a slot that is not the row's last key, a row with no keys, a new
+    slot in a block another sequence reads, a repeated slot.  Each must run as
+    write_kv then decode_attention (reshape_and_cache shows in the profile)
+    and give bitwise their output and pool contents."""
+    import torch
+    _say(f"decode+write_kv non-canonical: {case}")
+    heads, kvh, hd, bs = 32, 8, 128, 16
+    ctx = [40, 100, 17, 300]
+    runs = []
+    for _ in range(2):
+        backend = vo.HipBackend(device=0, max_seqs=8, max_rows=W.FILL_ROWS,
+                                max_table_entries=512, max_query_heads=heads)
+        wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=kvh, head_dim=hd,
+                     block_size=bs, num_blocks=200, context_lens=ctx, seed=77)
+        runs.append((backend, wl))
+    base = runs[0][1].meta
+    tables = [np.array(t, np.uint32) for t in base.block_tables]
+    rseq = np.array(base.row_seq, np.uint64)
+    rkeys = np.array(base.row_num_keys, np.uint64)
+    slots = np.array(base.slot_mapping, np.uint32)
+    pos = np.array(base.positions, np.uint32)
+    used = {int(b) for t in tables for b in t}
+    spare = next(b for b in range(200) if b not in used)
+    if case == "two_rows_one_seq":
+        rseq[1], rkeys[1] = 0, 30            # a second row of sequence 0, inside its keys
+        slots[1] = int(tables[0][29 // bs]) * bs + 29 % bs
+    elif case == "slot_not_last_key":
+        slots[2] = spare * bs + 3            # a block no table holds
+    elif case == "zero_keys":
+        rkeys[3] = 0
+    elif case == "tail_block_shared":
+        tables[1] = tables[1].copy()
+        tables[1][0] = tables[0][40 // bs]   # sequence 1 reads the block of sequence 0's new slot
+    elif case == "repeated_slot":
+        slots[3] = slots[2]
+    meta = vo.DecodeMeta(bs, tables, pos, slots, rseq, rkeys)
+    results = []
+    for i, (backend, wl) in enumerate(runs):
+        # The new slots first hold other values, so a launch that skipped the
+        # cache write, or read a slot it also writes, would differ.
+        gen = torch.Generator(device="cuda:0").manual_seed(9)
+        junk_k = torch.randn(wl.k_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
+        junk_v = torch.randn(wl.v_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
+        backend.write_kv(wl.pool, 0, junk_k, junk_v, wl.meta)
+        vo.profile_reset()
+        vo.enable_profiling(True)
+        if i == 0:
+            backend.write_kv(wl.pool, 0, wl.k_new, wl.v_new, meta)
+            out = backend.decode_attention(wl.q, wl.pool, 0, meta)
+        else:
+            out = backend.decode_attention_write_kv(wl.q, wl.k_new, wl.v_new, wl.pool, 0, meta)
+        torch.cuda.synchronize()
+        vo.enable_profiling(False)
+        kernels = set(vo.profile())
+        assert "reshape_and_cache" in kernels, (case, kernels)
+        pool_bits = []
+        for s_ in range(len(ctx)):
+            k, v = backend.read_kv(wl.pool, 0, meta, s_, ctx[s_] + 1)
+            pool_bits.append((_bits(k), _bits(v)))
+        results.append((_bits(out), pool_bits))
+    assert np.array_equal(results[0][0], results[1][0]), case
+    for s_ in range(len(ctx)):
+        assert np.array_equal(results[0][1][s_][0], results[1][1][s_][0]), (case, "K", s_)
+        assert np.array_equal(results[0][1][s_][1], results[1][1][s_][1]), (case, "V", s_)
+
+
 def test_decode_cfg2_full_size(vo, gpu_backend):
     """BASELINE config 2 at full size: 64 seqs, ctx U[512, 4096], 20000-block pool."""
     _say("decode cfg2 full size")

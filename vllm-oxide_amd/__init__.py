@@ -32,7 +32,7 @@ __all__ = [
     "LIB_PATH", "lib", "KvLayout", "slot_of", "PrefillSeq", "PrefillMeta", "DecodeSeq",
     "DecodeMeta", "EngineError", "ShapeError", "CapacityError", "BlockTableTooShort",
     "SlotOutOfRange", "BlockOutOfRange", "DeviceError", "InvalidArgument", "Unsupported",
-    "HipBackend", "KvPool", "StepMeta",
+    "HipBackend", "KvPool", "StepMeta", "Workspace", "Weight", "Region", "OutsideWorkspace",
 ]
 
 _HERE = pathlib.Path(__file__).resolve().parent
@@ -52,6 +52,7 @@ VO_ERR_INVALID_ARGUMENT = 7
 VO_ERR_UNSUPPORTED = 8
 VO_ERR_POSITION_OUT_OF_RANGE = 9
 VO_ERR_NAN = 10
+VO_ERR_OUTSIDE_WORKSPACE = 11
 VO_DTYPE_BF16 = 0
 VO_DTYPE_F32 = 1
 
@@ -168,6 +169,19 @@ SIGNATURES = {
     "vo_gemm_destroy": (None, [_vp]),
     "vo_matmul": (ctypes.c_int32, [_vp, _vp, _u64, _u64, _vp, _u64, _u64, _vp, ctypes.c_int32,
                                    ctypes.c_int32, _vp]),
+    "vo_workspace_create": (ctypes.c_int32, [ctypes.c_int32, _u64, ctypes.POINTER(_vp)]),
+    "vo_workspace_destroy": (None, [_vp]),
+    "vo_workspace_elems": (_u64, [_vp]),
+    "vo_workspace_region": (ctypes.c_int32, [_vp, _u64, _u64, _u64, ctypes.POINTER(_vp)]),
+    "vo_workspace_read": (ctypes.c_int32, [_vp, _u64, _u64, _u64, ctypes.c_int32,
+                                           ctypes.POINTER(ctypes.c_float), _vp]),
+    "vo_weight_upload": (ctypes.c_int32, [ctypes.c_int32, ctypes.POINTER(ctypes.c_float), _u64p,
+                                          _u64, ctypes.c_int32, ctypes.POINTER(_vp)]),
+    "vo_weight_concat_rows": (ctypes.c_int32, [ctypes.POINTER(_vp), _u64, ctypes.POINTER(_vp)]),
+    "vo_weight_destroy": (None, [_vp]),
+    "vo_weight_shape": (ctypes.c_int32, [_vp, _u64p, _u64, _u64p]),
+    "vo_weight_data": (_vp, [_vp]),
+    "vo_weight_dtype": (ctypes.c_int32, [_vp]),
     "vo_profiling_enable": (ctypes.c_int32, [ctypes.c_int32]),
     "vo_profile_read": (ctypes.c_int32, [ctypes.POINTER(vo_kernel_stat), _u64, _u64p]),
     "vo_profile_reset": (None, []),
@@ -242,6 +256,7 @@ class InvalidArgument(EngineError): pass
 class Unsupported(EngineError): pass
 class PositionOutOfRange(EngineError): pass
 class NaNError(EngineError): pass
+class OutsideWorkspace(EngineError): pass
 
 
 _ERROR_CLASSES = {
@@ -250,6 +265,7 @@ _ERROR_CLASSES = {
     VO_ERR_BLOCK_OUT_OF_RANGE: BlockOutOfRange, VO_ERR_DEVICE: DeviceError,
     VO_ERR_INVALID_ARGUMENT: InvalidArgument, VO_ERR_UNSUPPORTED: Unsupported,
     VO_ERR_POSITION_OUT_OF_RANGE: PositionOutOfRange, VO_ERR_NAN: NaNError,
+    VO_ERR_OUTSIDE_WORKSPACE: OutsideWorkspace,
 }
 
 
@@ -586,6 +602,111 @@ def _any_ptr(t, dtype) -> _vp:
     if t.dtype != dtype or not t.is_contiguous():
         raise TypeError(f"expected a contiguous {dtype} tensor, got {t.dtype}")
     return _vp(t.data_ptr())
+
+
+@dataclass(frozen=True)
+class Region:
+    """mod.rs:31-38: a [rows, cols] matrix at ``offset`` elements of the workspace."""
+    offset: int
+    rows: int
+    cols: int
+
+    def __len__(self) -> int:
+        return self.rows * self.cols
+
+
+class Workspace:
+    """Backend::alloc_workspace / workspace_elems / read (mod.rs:76-78,
+    177-181): the activation workspace, ``elems`` 4-byte elements of device
+    memory owned by the library (vo_workspace)."""
+
+    def __init__(self, elems: int, device: int = 0):
+        self._h = _vp()
+        _check(lib.vo_workspace_create(device, elems, ctypes.byref(self._h)))
+
+    @property
+    def handle(self):
+        return self._h
+
+    def elems(self) -> int:
+        return int(lib.vo_workspace_elems(self._h))
+
+    def ptr(self, region: Region) -> _vp:
+        """Device address of a region (OutsideWorkspace past the end)."""
+        out = _vp()
+        _check(lib.vo_workspace_region(self._h, region.offset, region.rows, region.cols,
+                                       ctypes.byref(out)))
+        return out
+
+    def read(self, region: Region, dtype: int = VO_DTYPE_F32, stream=0) -> np.ndarray:
+        """Backend::read: the region's values as f32 [rows, cols] (waits for ``stream``)."""
+        out = np.zeros(max(len(region), 1), np.float32)
+        _check(lib.vo_workspace_read(self._h, region.offset, region.rows, region.cols, dtype,
+                                     out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                     _vp(stream) if isinstance(stream, int) else _stream_ptr(stream)))
+        return out[:len(region)].reshape(region.rows, region.cols)
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_workspace_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Weight:
+    """Backend::upload / weight_shape (mod.rs:69-72): a weight the library
+    holds on the device (vo_weight), bf16 by default."""
+
+    def __init__(self, data=None, device: int = 0, dtype: int = VO_DTYPE_BF16, _handle=None):
+        self._h = _vp()
+        if _handle is not None:
+            self._h = _handle
+            return
+        a = np.ascontiguousarray(np.asarray(data, np.float32))
+        shape = _u64a(a.shape)
+        _check(lib.vo_weight_upload(device, a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                    _p64(shape), a.ndim, dtype, ctypes.byref(self._h)))
+
+    @staticmethod
+    def concat_rows(parts: Sequence["Weight"]) -> "Weight":
+        arr = (_vp * len(parts))(*[p.handle for p in parts])
+        h = _vp()
+        _check(lib.vo_weight_concat_rows(arr, len(parts), ctypes.byref(h)))
+        return Weight(_handle=h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def ptr(self) -> _vp:
+        return _vp(lib.vo_weight_data(self._h))
+
+    def shape(self) -> tuple:
+        n = ctypes.c_uint64()
+        _check(lib.vo_weight_shape(self._h, None, 0, ctypes.byref(n)))
+        dims = np.zeros(max(n.value, 1), np.uint64)
+        _check(lib.vo_weight_shape(self._h, _p64(dims), n.value, ctypes.byref(n)))
+        return tuple(int(d) for d in dims[:n.value])
+
+    def dtype(self) -> int:
+        return int(lib.vo_weight_dtype(self._h))
+
+    def close(self) -> None:
+        if self._h:
+            lib.vo_weight_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class BlockManager:

@@ -117,7 +117,7 @@ class Packer {
             return sinks_.back().data();
         }
         *device_ptr = reinterpret_cast<const uint32_t *>(m_->d_buf + at);
-        return reinterpret_cast<uint32_t *>(m_->h_stage + at);
+        return reinterpret_cast<uint32_t *>(m_->stage.current() + at);
     }
     uint64_t used() const { return off_; }
     bool fits() const { return !overflow_; }
@@ -131,23 +131,19 @@ class Packer {
     std::vector<std::vector<uint32_t>> sinks_;
 };
 
-vo_status wait_previous_copy(vo_step_meta *m, const char *op) {
-    if (m->copy_pending) {
-        hipError_t err = hipEventSynchronize(m->copy_done);
-        if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
-        m->copy_pending = false;
-    }
+// Takes the staging buffer this upload fills (double-buffered: the host
+// waits only if the copy out of it, two uploads ago, has not run yet).
+vo_status acquire_staging(vo_step_meta *m, const char *op) {
+    uint8_t *host;
+    const hipError_t err = m->stage.acquire(&host);
+    if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
     return VO_OK;
 }
 
 vo_status finish_upload(vo_step_meta *m, const Packer &pk, hipStream_t stream, const char *op) {
     if (pk.used() > 0) {
-        hipError_t err = hipMemcpyAsync(m->d_buf, m->h_stage, pk.used(), hipMemcpyHostToDevice,
-                                        stream);
+        const hipError_t err = m->stage.commit(m->d_buf, pk.used(), stream);
         if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
-        err = hipEventRecord(m->copy_done, stream);
-        if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
-        m->copy_pending = true;
     }
     return VO_OK;
 }
@@ -202,7 +198,7 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
             return rc;
     }
     if (num_rows && !slot_mapping) return fail_argument(op, "null slot mapping");
-    if (vo_status rc = wait_previous_copy(m, op)) return rc;
+    if (vo_status rc = acquire_staging(m, op)) return rc;
 
     const uint64_t entries = table_off[num_seqs];
     m->kind = kind;
@@ -320,12 +316,16 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
 // slower on the last two.
 constexpr uint64_t kDefaultSplit = 2048;
 
-uint64_t decode_split_keys() {
+}  // namespace
+
+uint64_t vo::decode_split_keys() {
     const int env = env_int("VO_DECODE_SPLIT", 0);
     return (env >= 32 && env % 32 == 0 && env <= static_cast<int>(kernels::kMaxSplitKeys))
                ? static_cast<uint64_t>(env)
                : kDefaultSplit;
 }
+
+namespace {
 
 // True when no physical block is read by two sequences of this step (no
 // prefix sharing through aliased table entries): the decode kernel then
@@ -416,6 +416,25 @@ uint64_t pack_full_splits(vo_step_meta *m, uint32_t *work, uint64_t nfull, uint6
         ++n;
     }
     return n;
+}
+
+// Every row of the upload is the one DecodeMeta::new (paged.rs:189-209)
+// gives a sequence: one row per sequence, at least one key (the new one),
+// and the slot of its last key, slot_of(table, keys - 1) (paged.rs:47-52,
+// u32 arithmetic).  The upload accepts any rows, as the reference's pub
+// fields do; the one-launch write_kv + decode_attention needs these.
+bool canonical_decode_rows(vo_step_meta *m) {
+    const uint64_t bs = m->block_size;
+    m->block_seen.assign(m->num_seqs, 0);  // here: rows per sequence
+    for (uint64_t r = 0; r < m->num_rows; ++r) {
+        const uint32_t seq = m->row_seq[r];
+        const uint32_t nk = m->row_num_keys[r];
+        if (nk == 0 || m->block_seen[seq]) return false;
+        m->block_seen[seq] = 1;
+        // check_rows already made sure the table covers nk keys.
+        if (m->slots[r] != slot_of(m->tables.data() + m->table_off[seq], nk - 1, bs)) return false;
+    }
+    return true;
 }
 
 // Split-K plan over the rows listed in `rows` (every row of the step when
@@ -521,11 +540,16 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     // repeated slots or a fixed launch, and no block holding a new slot read
     // by another sequence (with a streaming plan no block is shared at all).
     // A packed item's blocks are read by several rows, so under these
-    // conditions it never holds a row's last key.
+    // conditions it never holds a row's last key.  Every row must also be
+    // the canonical decode row DecodeMeta::new builds (paged.rs:189-209):
+    // its own sequence, at least one key, and its slot the one of its last
+    // key.  Only then is the workgroup holding that key the one place that
+    // reads the slot, so taking K/V from the new rows and writing the slot at
+    // the end equals write_kv followed by decode_attention.
     m->fused_write_ok = false;
     if (!rows && !pk.fixed() && !m->slots_repeat && m->kind == kDecode) {
-        bool ok = true;
-        if (!streaming) {
+        bool ok = canonical_decode_rows(m);
+        if (ok && !streaming) {
             const uint64_t bs = m->block_size;
             m->seq_keys.assign(m->num_seqs, 0);
             for (uint64_t r = 0; r < T; ++r)
@@ -620,10 +644,14 @@ bool mixed_overlap_enabled() {
     return on;
 }
 
-int decode_waves() {
+}  // namespace
+
+int vo::decode_waves() {
     int w = env_int("VO_DECODE_WAVES", 4);
     return (w == 1 || w == 2 || w == 4 || w == 8) ? w : 4;
 }
+
+namespace {
 
 
 }  // namespace
@@ -700,21 +728,16 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
                           + 10 * 64;                                         // alignment slack
     m->buf_bytes = align_up(u32s * sizeof(uint32_t), 4096);
     hipError_t err = hipMalloc(reinterpret_cast<void **>(&m->d_buf), m->buf_bytes);
-    if (err == hipSuccess)
-        err = hipHostMalloc(reinterpret_cast<void **>(&m->h_stage), m->buf_bytes, hipHostMallocDefault);
+    if (err == hipSuccess) err = m->stage.create(m->buf_bytes);
     if (err == hipSuccess)
         err = hipMalloc(reinterpret_cast<void **>(&m->d_part_acc),
                         m->max_parts * max_query_heads * m->head_dim * sizeof(float));
     if (err == hipSuccess)
         err = hipMalloc(reinterpret_cast<void **>(&m->d_part_ml),
                         m->max_parts * max_query_heads * 2 * sizeof(float));
-    if (err == hipSuccess) err = hipEventCreateWithFlags(&m->copy_done, hipEventDisableTiming);
     if (err == hipSuccess)
         err = hipMalloc(reinterpret_cast<void **>(&m->d_tokens), max_rows * sizeof(uint32_t));
-    if (err == hipSuccess)
-        err = hipHostMalloc(reinterpret_cast<void **>(&m->h_tokens), max_rows * sizeof(uint32_t),
-                            hipHostMallocDefault);
-    if (err == hipSuccess) err = hipEventCreateWithFlags(&m->tokens_done, hipEventDisableTiming);
+    if (err == hipSuccess) err = m->tokens_stage.create(max_rows * sizeof(uint32_t));
     // Default priority, like every stream here.
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&m->fork, hipEventDisableTiming);
@@ -722,13 +745,11 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
     if (err != hipSuccess) {
         vo_status rc = fail_device(op, err, hipGetErrorString(err));
         if (m->d_tokens) (void)hipFree(m->d_tokens);
-        if (m->h_tokens) (void)hipHostFree(m->h_tokens);
-        if (m->tokens_done) (void)hipEventDestroy(m->tokens_done);
+        m->tokens_stage.destroy();
         if (m->d_buf) (void)hipFree(m->d_buf);
-        if (m->h_stage) (void)hipHostFree(m->h_stage);
+        m->stage.destroy();
         if (m->d_part_acc) (void)hipFree(m->d_part_acc);
         if (m->d_part_ml) (void)hipFree(m->d_part_ml);
-        if (m->copy_done) (void)hipEventDestroy(m->copy_done);
         if (m->side) (void)hipStreamDestroy(m->side);
         if (m->fork) (void)hipEventDestroy(m->fork);
         if (m->join) (void)hipEventDestroy(m->join);
@@ -743,14 +764,10 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
 extern "C" void vo_step_meta_destroy(vo_step_meta *m) {
     if (!m) return;
     DeviceGuard guard(m->device);
-    if (m->copy_pending) (void)hipEventSynchronize(m->copy_done);
-    if (m->copy_done) (void)hipEventDestroy(m->copy_done);
-    if (m->tokens_pending) (void)hipEventSynchronize(m->tokens_done);
-    if (m->tokens_done) (void)hipEventDestroy(m->tokens_done);
+    m->stage.destroy();
+    m->tokens_stage.destroy();
     (void)hipFree(m->d_tokens);
-    (void)hipHostFree(m->h_tokens);
     (void)hipFree(m->d_buf);
-    (void)hipHostFree(m->h_stage);
     (void)hipFree(m->d_part_acc);
     (void)hipFree(m->d_part_ml);
     if (m->side) {

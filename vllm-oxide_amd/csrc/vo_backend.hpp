@@ -97,9 +97,69 @@ struct FixedLaunch {
     uint64_t bytes = 0;
 };
 
+// Keys per split-K split of the decode kernels (a multiple of 32; the same
+// for every row and batch, so a row's arithmetic does not depend on the
+// batch) and wavefronts per decode workgroup.  VO_DECODE_SPLIT and
+// VO_DECODE_WAVES override them (tuning knobs).
+uint64_t decode_split_keys();
+int decode_waves();
+
 // A row's last, shorter split in the decode work order (keys < split size).
 struct TailItem {
     uint32_t keys, row, split;
+};
+
+// Pinned host staging of one kind of upload, double-buffered.  The host fills
+// one buffer while the copy out of the other may still be in flight, so an
+// upload waits on the host only when both buffers' copies are still pending
+// (a third upload before the first one's copy ran).
+struct Staging {
+    uint8_t *buf[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool pending[2] = {false, false};
+    int cur = 0;
+
+    hipError_t create(uint64_t bytes) {
+        for (int i = 0; i < 2; ++i) {
+            hipError_t err = hipHostMalloc(reinterpret_cast<void **>(&buf[i]), bytes, hipHostMallocDefault);
+            if (err == hipSuccess) err = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
+            if (err != hipSuccess) return err;
+        }
+        return hipSuccess;
+    }
+    void destroy() {
+        for (int i = 0; i < 2; ++i) {
+            if (pending[i] && done[i]) (void)hipEventSynchronize(done[i]);
+            if (done[i]) (void)hipEventDestroy(done[i]);
+            if (buf[i]) (void)hipHostFree(buf[i]);
+            buf[i] = nullptr;
+            done[i] = nullptr;
+            pending[i] = false;
+        }
+    }
+    // The buffer the next upload fills.  Its last copy was enqueued two
+    // uploads ago; the host waits only if that copy has not run yet.
+    hipError_t acquire(uint8_t **host) {
+        if (pending[cur]) {
+            hipError_t err = hipEventQuery(done[cur]);
+            if (err == hipErrorNotReady) err = hipEventSynchronize(done[cur]);
+            if (err != hipSuccess) return err;
+            pending[cur] = false;
+        }
+        *host = buf[cur];
+        return hipSuccess;
+    }
+    uint8_t *current() const { return buf[cur]; }
+    // Copies the first `bytes` of the current buffer to `dst` on `stream`
+    // and moves on to the other buffer.
+    hipError_t commit(void *dst, uint64_t bytes, hipStream_t stream) {
+        hipError_t err = hipMemcpyAsync(dst, buf[cur], bytes, hipMemcpyHostToDevice, stream);
+        if (err == hipSuccess) err = hipEventRecord(done[cur], stream);
+        if (err != hipSuccess) return err;
+        pending[cur] = true;
+        cur ^= 1;
+        return hipSuccess;
+    }
 };
 
 }  // namespace vo
@@ -149,12 +209,10 @@ struct vo_step_meta {
     std::vector<uint32_t> positions;    // [T] when uploaded
     uint32_t max_position = 0;          // largest position (0 if none)
 
-    // Device buffer and pinned staging of the same size.
+    // Device buffer and its pinned staging (two buffers of the same size).
     uint8_t *d_buf = nullptr;
-    uint8_t *h_stage = nullptr;
+    vo::Staging stage;
     uint64_t buf_bytes = 0;
-    hipEvent_t copy_done = nullptr;
-    bool copy_pending = false;
     // A mixed step's decode rows run on `side`, forked from and joined back
     // into the caller's stream, beside the prefill chunks.
     hipStream_t side = nullptr;
@@ -198,9 +256,7 @@ struct vo_step_meta {
     // copy for the kernel, pinned staging for the copy.
     std::vector<uint32_t> tokens;
     uint32_t *d_tokens = nullptr;   // [max_rows]
-    uint32_t *h_tokens = nullptr;   // [max_rows], pinned
-    hipEvent_t tokens_done = nullptr;
-    bool tokens_pending = false;
+    vo::Staging tokens_stage;       // 2 x [max_rows], pinned
     bool has_tokens = false;
 };
 

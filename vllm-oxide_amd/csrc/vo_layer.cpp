@@ -30,21 +30,19 @@ extern "C" int32_t vo_step_meta_upload_tokens(vo_step_meta *m, const uint32_t *t
     if (num_tokens > m->max_rows) return fail_capacity("tokens per step", num_tokens, m->max_rows);
     if (num_tokens && !tokens) return fail_argument(op, "null tokens");
     DeviceGuard guard(m->device);
-    if (m->tokens_pending) {
-        // The staging buffer is reused: the previous copy must have left it.
-        hipError_t err = hipEventSynchronize(m->tokens_done);
-        if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
-        m->tokens_pending = false;
-    }
     m->tokens.assign(tokens, tokens + num_tokens);
     m->has_tokens = true;
     if (num_tokens) {
-        std::memcpy(m->h_tokens, tokens, num_tokens * sizeof(uint32_t));
-        hipError_t err = hipMemcpyAsync(m->d_tokens, m->h_tokens, num_tokens * sizeof(uint32_t),
-                                        hipMemcpyHostToDevice, static_cast<hipStream_t>(stream));
-        if (err == hipSuccess) err = hipEventRecord(m->tokens_done, static_cast<hipStream_t>(stream));
+        // Double-buffered pinned staging: waits only if the copy out of this
+        // buffer, two uploads ago, has not run yet.
+        uint8_t *host;
+        hipError_t err = m->tokens_stage.acquire(&host);
+        if (err == hipSuccess) {
+            std::memcpy(host, tokens, num_tokens * sizeof(uint32_t));
+            err = m->tokens_stage.commit(m->d_tokens, num_tokens * sizeof(uint32_t),
+                                         static_cast<hipStream_t>(stream));
+        }
         if (err != hipSuccess) return fail_device(op, err, hipGetErrorString(err));
-        m->tokens_pending = true;
     }
     clear_error();
     return VO_OK;

@@ -227,6 +227,7 @@ extern "C" const char *vo_status_name(int32_t status) {
         case VO_ERR_UNSUPPORTED: return "VO_ERR_UNSUPPORTED";
         case VO_ERR_POSITION_OUT_OF_RANGE: return "VO_ERR_POSITION_OUT_OF_RANGE";
         case VO_ERR_NAN: return "VO_ERR_NAN";
+        case VO_ERR_OUTSIDE_WORKSPACE: return "VO_ERR_OUTSIDE_WORKSPACE";
         default: return "VO_ERR_UNKNOWN";
     }
 }
