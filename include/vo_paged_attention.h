@@ -379,6 +379,33 @@ int32_t vo_decode_attention(const void *queries, uint64_t rows, uint64_t cols,
                             const vo_kv_pool *pool, uint64_t layer, const vo_step_meta *meta,
                             void *out, void *stream);
 
+/* Decode attention that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The op is
+ * Backend::decode_attention (mod.rs:137-149) on the kernels of
+ * vo_decode_attention, and its output is bitwise that entry point's; but the
+ * decode step's metadata is read from device memory the caller owns, in
+ * DecodeMeta::new's layout (paged.rs:189-209: row s is sequence s): table_off
+ * [rows+1] CSR offsets into tables [num_entries], row_num_keys [rows]
+ * (context + 1), all device u32 arrays, and no vo_step_meta is needed.  The
+ * split-K plan and partials live in a fixed 32 MiB device array per GPU,
+ * which bounds a call: rows <= 4096 and rows * ceil(max_keys / 2048) work
+ * items of partials (num_heads * head_dim fp32 each) within 32 MiB, else
+ * VO_ERR_CAPACITY before anything is enqueued (e.g. 256 rows of up to 8192
+ * keys at 32 heads of 128 dims fit).  max_keys bounds every row's key count.
+ * The host checks shapes and sizes; the device checks, before any pool read,
+ * what vo_decode_attention checks on the host -- coverage (paged.rs:64-80),
+ * every table entry < num_blocks (attention.rs:130-147) -- plus keys <=
+ * max_keys and offsets ascending within num_entries; on a failure it sets
+ * *errors (a device u32 the call does not clear) to 1 and writes zero rows.
+ * Calls that overlap on one GPU (other streams, other threads) share its
+ * array and race.  Needs block size 16, head_dim 64 or 128, group <= 16. */
+int32_t vo_decode_attention_static(const void *queries, uint64_t rows, uint64_t cols,
+                                   const vo_kv_pool *pool, uint64_t layer, const uint32_t *table_off,
+                                   const uint32_t *tables, uint64_t num_entries,
+                                   const uint32_t *row_num_keys, uint64_t max_keys, void *out,
+                                   uint32_t *errors, void *stream);
+
 /* Debug and test only (the counterpart of Backend::read, mod.rs:177-181):
  * gather keys 0..num_keys of sequence `seq` of the last upload in `meta` from
  * `layer` into out_keys and out_values, each [num_keys, kv_heads * head_dim]

@@ -130,6 +130,8 @@ SIGNATURES = {
     "vo_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _vp, _vp]),
     "vo_prefill_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
     "vo_decode_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
+    "vo_decode_attention_static": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _u64,
+                                                    _vp, _u64, _vp, _vp, _vp]),
     "vo_gather_kv": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _vp, _vp, _vp]),
     "vo_prefill_meta_build_device": (ctypes.c_int32, [_vp, _vp, _vp, _vp, _u64, _u64, _u64,
                                                       _vp, _vp, _vp, _vp, _vp, _vp]),
