@@ -480,6 +480,61 @@ def test_prefill_chunked_with_context(vo, gpu_backend, hd, heads, kvh):
     _assert_close(out.float().cpu().numpy(), want, f"prefill hd={hd}")
 
 
+@pytest.mark.parametrize("offset", ["fixed", "running"])
+def test_prefill_64_row_workgroups_edge_shapes(vo, gpu_backend, monkeypatch, offset):
+    """The 64-row workgroups at GQA 4, head_dim 128, with the fixed tile-0
+    softmax offset and with the running max (VO_PREFILL_OFFSET), on a grid
+    small enough that the 32-row workgroups would otherwise serve it
+    (VO_PREFILL_NARROW=0): chunks starting at 0, mid-block, on and next to
+    tile boundaries; items of 2, 31, 32, 33, 64 and 65 rows; one row per
+    block of a 2047-key context."""
+    _say(f"prefill 64-row workgroups ({offset} offset)")
+    monkeypatch.setenv("VO_PREFILL_NARROW", "0")
+    monkeypatch.setenv("VO_PREFILL_OFFSET", offset)
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=1200,
+                 context_lens=[0, 5, 63, 64, 65, 1000, 2047, 31],
+                 num_new=[2, 31, 32, 33, 64, 65, 129, 200], seed=61)
+    gpu_backend.step_meta(wl.pool).holds = None
+    out = _out(wl, gpu_backend)
+    want = W.oracle_attention(orc, wl)
+    _assert_close(out.float().cpu().numpy(), want, f"prefill 64-row workgroups ({offset})")
+
+
+@pytest.mark.parametrize("narrow", ["1", "0"])
+@pytest.mark.parametrize("factor", [4.0, 10.0])
+def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, factor):
+    """The prefill kernel first keeps each row's tile-0 max as its softmax
+    offset.  Key 200 of sequence 0 (cached, KV tile 3) is set to factor x
+    query row 0's head-0 vector (KV head 0 serves heads 0..3), so that row's
+    score for it is ~factor |q|^2 / sqrt(128): ~65 log2 units above the rest
+    at factor 4 (row sum past the 2^40 bound, no overflow yet) and ~163 at
+    factor 10, where 2^163 overflows f32 and only the recompute with the
+    running max gives finite output.  Every row must match the oracle, in
+    32-row (narrow) and 64-row workgroups."""
+    import torch
+    _say(f"prefill key far above tile-0 max (factor {factor}, narrow {narrow})")
+    monkeypatch.setenv("VO_PREFILL_NARROW", narrow)
+    ctx, new = [300, 0, 900], [64, 128, 100]
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=200, context_lens=ctx, num_new=new, seed=62)
+    q0 = wl.q[0, :128].float()
+    k_big = (factor * q0).to(torch.bfloat16)
+    keys = wl.ctx_kv[0][0].clone()
+    keys[200, :128] = k_big
+    slot = int(wl.tables[0][200 // 16]) * 16 + 200 % 16
+    gpu_backend.write_kv(wl.pool, 0, keys[200:201].contiguous(),
+                         wl.ctx_kv[0][1][200:201].contiguous(), [slot])
+    wl.ctx_kv[0] = (keys, wl.ctx_kv[0][1])
+    wl.host["ctx"][0] = (keys.float().cpu().numpy(), wl.host["ctx"][0][1])
+    gpu_backend.step_meta(wl.pool).holds = None
+    out = _out(wl, gpu_backend)
+    want = W.oracle_attention(orc, wl)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    _assert_close(got, want, f"prefill key far above tile-0 max (factor {factor})")
+
+
 def test_prefill_cfg3_full_size_sampled_rows(vo, gpu_backend):
     """8 seqs x 512-row chunks on context U[0, 8192]; every
     row is computed on the GPU, a sample of rows by the oracle."""

@@ -35,7 +35,10 @@
 //                    exceeds it by more than kLazyLog2 (the accumulators are
 //                    rescaled then); otherwise the tile reuses the stale m,
 //                    which leaves numerator and denominator scaled alike and
-//                    keeps P <= 2^kLazyLog2.
+//                    keeps P <= 2^kLazyLog2.  The DMA kernel first runs with
+//                    m fixed at the tile-0 max (no max or rescale after tile
+//                    0) and falls back to the running max for a workgroup
+//                    whose row sums leave the range that proves it exact.
 //   O^T += V^T . P^T B = P^T is then exactly the lane's own probabilities:
 //                    16-key step j uses registers 8*(j&1) .. +7 of half j>>1.
 //                    A = 32 dims x 16 keys of V^T from LDS.  Output rows are
@@ -76,6 +79,9 @@ constexpr int kQT = 64;          // query rows per work item
 constexpr int kRG = 32;          // query rows per wavefront
 constexpr int kKT = 64;          // keys per KV tile (4 blocks)
 constexpr float kLazyLog2 = 8.0f;  // growth of a row max (log2 units) absorbed without a rescale
+// Row sum below which a fixed-offset pass provably kept every P and O in
+// range (2^40; see prefill_dma_kernel).
+constexpr float kOverflowSum = 1099511627776.0f;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -428,7 +434,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
     const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
     const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
-    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2) {
+    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2, uint32_t fixed_offset) {
     constexpr int W = G * R;
     constexpr int HALVES = kQT / (kRG * R);
     using D = DmaShape<HD, W>;
@@ -441,6 +447,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     __shared__ __align__(1024) uint8_t st0[D::STAGE];
     __shared__ __align__(1024) uint8_t st1[D::STAGE];
     __shared__ __align__(1024) uint8_t st2[D::STAGE];
+    __shared__ uint32_t redo;  // set when a row of the fixed-offset pass left its range
 
     const uint32_t kvh = blockIdx.x % kv_heads;
     const uint32_t rest = blockIdx.x / kv_heads;
@@ -472,6 +479,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     const uint32_t wp_max = min(wp_min + kRG - 1, p_max);
 
     for (uint32_t i = tid; i < nblk; i += 64 * W) tbl[i] = table[i];
+    if (tid == 0) redo = 0u;
 
     bf16x8 qv[KS];
     {
@@ -531,8 +539,9 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     // The stage read and the stage filled are passed as restrict pointers, so
     // the compiler knows this step's DMA does not write what it reads (it
     // then inserts no wait for that DMA before the reads).
-    auto body = [&](auto first_c, uint32_t t, const uint8_t *__restrict__ tile,
+    auto body = [&](auto fixed_c, auto first_c, uint32_t t, const uint8_t *__restrict__ tile,
                     uint8_t *__restrict__ ahead) __attribute__((always_inline)) {
+        constexpr bool fixed = decltype(fixed_c)::value;
         constexpr bool first = decltype(first_c)::value;
         // Every step issues its DMA, past the last tile too (block ids clamp
         // to the table's last entry), so that every step has the same number
@@ -569,20 +578,26 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
                 sc[r] = (key <= p_row) ? sc[r] : -INFINITY;
             }
         }
-        float mx = sc[0];
+        // Row max of the tile, in the exp2 domain (both lanes of the row).
+        auto tile_max = [&]() __attribute__((always_inline)) {
+            float mx = sc[0];
 #pragma unroll
-        for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mt = mx * scale_log2;
+            for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            return mx * scale_log2;
+        };
         if constexpr (first) {
-            m_run = mt;
-        } else if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazyLog2) != 0) {
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
+            m_run = tile_max();  // finite: every row sees key 0
+        } else if constexpr (!fixed) {
+            const float mt = tile_max();
+            if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazyLog2) != 0) {
+                const float m_new = fmaxf(m_run, mt);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
-            m_run = m_new;
+                for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
+                m_run = m_new;
+            }
         }
         const float nm = -m_run;
 #pragma unroll
@@ -614,11 +629,11 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         // Tile t + 1 must have landed; tile t + 2 (this step's DMA) may fly on.
         wait_barrier<DPW>();
     };
-    auto step = [&](auto buf_c, auto first_c, uint32_t t) {
+    auto step = [&](auto fixed_c, auto buf_c, auto first_c, uint32_t t) {
         constexpr int buf = decltype(buf_c)::value;
-        if constexpr (buf == 0) body(first_c, t, st0, st2);
-        else if constexpr (buf == 1) body(first_c, t, st1, st0);
-        else body(first_c, t, st2, st1);
+        if constexpr (buf == 0) body(fixed_c, first_c, t, st0, st2);
+        else if constexpr (buf == 1) body(fixed_c, first_c, t, st1, st0);
+        else body(fixed_c, first_c, t, st2, st1);
     };
 
     using B0 = std::integral_constant<int, 0>;
@@ -627,26 +642,56 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     using First = std::integral_constant<bool, true>;
     using Rest = std::integral_constant<bool, false>;
 
-    dma_tile(st0, blk_of(0, 0), blk_of(0, 1), blk_of(0, 2), blk_of(0, 3));
-    dma_tile(st1, blk_of(1, 0), blk_of(1, 1), blk_of(1, 2), blk_of(1, 3));
-    n0 = blk_of(2, 0);
-    n1 = blk_of(2, 1);
-    n2 = blk_of(2, 2);
-    n3 = blk_of(2, 3);
-    wait_barrier<DPW>();
-    step(B0{}, First{}, 0);
-    for (uint32_t t = 1; t < n_tiles; t += 3) {
-        step(B1{}, Rest{}, t);
-        if (t + 1 >= n_tiles) break;
-        step(B2{}, Rest{}, t + 1);
-        if (t + 2 >= n_tiles) break;
-        step(B0{}, Rest{}, t + 2);
-    }
-    // The DMA of the tiles past the end is still in flight: it must land
-    // before the workgroup's LDS is released.
-    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    // One pass over the item's KV tiles; m_run, l_run and o_acc start afresh.
+    auto pass = [&](auto fixed_c) __attribute__((always_inline)) {
+        m_run = 0.0f;
+        l_run = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
+        dma_tile(st0, blk_of(0, 0), blk_of(0, 1), blk_of(0, 2), blk_of(0, 3));
+        dma_tile(st1, blk_of(1, 0), blk_of(1, 1), blk_of(1, 2), blk_of(1, 3));
+        n0 = blk_of(2, 0);
+        n1 = blk_of(2, 1);
+        n2 = blk_of(2, 2);
+        n3 = blk_of(2, 3);
+        wait_barrier<DPW>();
+        step(fixed_c, B0{}, First{}, 0);
+        for (uint32_t t = 1; t < n_tiles; t += 3) {
+            step(fixed_c, B1{}, Rest{}, t);
+            if (t + 1 >= n_tiles) break;
+            step(fixed_c, B2{}, Rest{}, t + 1);
+            if (t + 2 >= n_tiles) break;
+            step(fixed_c, B0{}, Rest{}, t + 2);
+        }
+        // The DMA of the tiles past the end is still in flight: it must land
+        // before the stages are refilled or the workgroup's LDS is released.
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+        l_run += __shfl_xor(l_run, 32, 64);
+    };
 
-    l_run += __shfl_xor(l_run, 32, 64);
+    // Fixed softmax offset: m_run stays at the row's tile-0 max.  A later
+    // score above it gives P = 2^(s c - m) > 1, which bf16 and the f32 sums
+    // hold with the same relative precision, and O / l does not depend on
+    // the offset; so later tiles need neither a row max nor a rescale.  Only
+    // the range can fail: every P is a term of l, and |O| <= l max |V|, so a
+    // row with l below kOverflowSum and a finite O lost nothing.  If any row
+    // of the workgroup is past that, the workgroup recomputes its item with
+    // the running max (raised by more than kLazyLog2 at a time) and writes
+    // that result instead.
+    if (fixed_offset) {
+        pass(std::true_type{});
+        bool ok = l_run < kOverflowSum;  // false for inf and NaN too
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ok = ok && __builtin_isfinite(o_acc[dt][r]);
+        if (__builtin_amdgcn_ballot_w64(row_ok && !ok) != 0 && lane == 0) redo = 1u;
+    } else if (tid == 0) {
+        redo = 1u;
+    }
+    wait_barrier<0>();
+    if (uniform_u32(redo) != 0) pass(std::false_type{});
+
     if (!row_ok) return;
     const float inv = 1.0f / l_run;
     uint16_t *op = out + (static_cast<uint64_t>(row_begin + lr) * num_heads + qhead) * HD + 4 * gl;
@@ -671,6 +716,14 @@ bool prefill_use_dma() {
         return !(v && std::string(v) == "regs");
     }();
     return dma;
+}
+
+// VO_PREFILL_OFFSET=running runs the DMA kernel with the running row max
+// from the start instead of the fixed tile-0 offset (A/B).  Read at every
+// launch.
+bool prefill_fixed_offset() {
+    const char *v = std::getenv("VO_PREFILL_OFFSET");
+    return !(v && std::string(v) == "running");
 }
 
 // VO_PREFILL_NARROW=0 keeps 64-row workgroups on small grids (A/B).
@@ -700,7 +753,7 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
             hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
                                dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
                                meta.table_off, meta.tables, plan.work, q, out, num_heads,
-                               scale_log2);
+                               scale_log2, prefill_fixed_offset() ? 1u : 0u);
             return hipGetLastError();
         }
     }
