@@ -237,38 +237,58 @@ def test_decode_streaming_loads_bitwise_equal(vo, monkeypatch):
         _assert_close(got, want, f"streaming shared={shared}")
 
 
-@pytest.mark.parametrize("hd,heads,kvh,split,waves", [
-    (128, 64, 8, "1024", "4"),  # cfg5's shape: group 8, two rows per item
-    (128, 32, 8, "512", "1"),   # group 4, four rows per item, no LDS merge
-    (64, 6, 2, "256", "2"),     # group 3, five rows per item, a short last pack
+@pytest.mark.parametrize("hd,heads,kvh,split,waves,mode,nalias", [
+    (128, 64, 8, "1024", "4", 1, 12),  # cfg5's shape: group 8, two rows per item
+    (128, 64, 8, "1024", "4", 2, 12),  # shared packs: 4 wavefronts x 2 rows
+    (128, 64, 8, "2048", "4", 2, 2),   # a shared pack of 2 of its 8 rows
+    (128, 64, 8, "2048", "4", 2, 1),   # no two rows share a split: nothing packed
+    (128, 32, 8, "512", "1", 1, 12),   # group 4, four rows per item, no LDS merge
+    (128, 32, 8, "512", "1", 2, 12),   # one wavefront: shared packs fall back to one tile
+    (128, 32, 8, "512", "8", 2, 12),   # 8 wavefronts: shared packs fall back to one tile
+    (128, 32, 8, "512", "4", 2, 12),   # 4 wavefronts x 4 rows: one pack of 12 of 16 rows
+    (64, 6, 2, "256", "2", 1, 12),     # group 3, five rows per item, a short last pack
+    (64, 6, 2, "256", "4", 2, 12),     # group 3, shared: 4 wavefronts x 5 rows
 ])
-def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, waves):
+def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, waves, mode,
+                                    nalias):
     """Rows whose full splits read the same physical blocks (an aliased
-    prefix) share one work item, each row in its own head columns of the
-    MFMA tile.  The outputs are bitwise those of the unpacked plan
+    prefix) share one work item, each row in its own head columns: one
+    16-column MFMA tile per item (VO_DECODE_PACK=1), or a shared pack whose 4
+    wavefronts each take a tile over chunks staged once in LDS (=2, the
+    default).  The outputs are bitwise those of the unpacked plan
     (VO_DECODE_PACK=0) and within tolerance of the oracle; the plan really
-    packs: each of the two shared prefix splits of the 12 aliasing rows runs
-    as ceil(12 / P) items."""
+    packs: each of the two shared prefix splits of the aliasing rows runs as
+    ceil(rows / P) items, with P rows per item for the mode."""
     monkeypatch.setenv("VO_DECODE_SPLIT", split)
     monkeypatch.setenv("VO_DECODE_WAVES", waves)
-    _say(f"decode row packing hd={hd} heads={heads} kvh={kvh} split={split} waves={waves}")
+    _say(f"decode row packing hd={hd} heads={heads} kvh={kvh} split={split} waves={waves} "
+         f"mode={mode} aliasing rows={nalias}")
     L = int(split)
     backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=8192,
                             max_query_heads=heads)
     shared = 2 * L
-    extra = [0, 1, 17, 100, L - 1, L, L + 5, 5, 2 * L + 3, 64, 700 % L, 31]
+    extra = [0, 1, 17, 100, L - 1, L, L + 5, 5, 2 * L + 3, 64, 700 % L, 31][:nalias]
     ctx = [shared + e for e in extra] + [3 * L, 50]
     wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=kvh, head_dim=hd,
                  block_size=16, num_blocks=4000, context_lens=ctx, seed=L + heads,
                  shared_prefix=shared, shared_count=len(extra))
-    P = 16 // (heads // kvh)
+    group = heads // kvh
+    one_tile = 16 // group
+    if mode == 2 and int(waves) != 4:
+        mode = 1  # shared packs need 4 wavefronts
+    if mode == 1:
+        P = one_tile
+    else:
+        P = 4 * (16 // group)
+        if min(P, len(extra)) < 2:
+            P = 1  # nothing to share
     parts = sum(-(-(c + 1) // L) for c in ctx)
     meta = backend.step_meta(wl.pool)
 
     monkeypatch.setenv("VO_DECODE_PACK", "0")
     plain = _out_replanned(wl, backend)
     assert meta.decode_plan() == (parts, parts, 1)
-    monkeypatch.delenv("VO_DECODE_PACK")
+    monkeypatch.setenv("VO_DECODE_PACK", str(mode))
     packed = _out_replanned(wl, backend)
     packs = -(-len(extra) // P)
     assert meta.decode_plan() == (parts - 2 * (len(extra) - packs), parts, P)
@@ -276,7 +296,7 @@ def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, wave
     again = _out(wl, backend)
     assert np.array_equal(_bits(again), _bits(packed))
     want = W.oracle_attention(orc, wl)
-    _assert_close(packed.float().cpu().numpy(), want, f"packed hd={hd} H={heads}")
+    _assert_close(packed.float().cpu().numpy(), want, f"packed hd={hd} H={heads} mode={mode}")
 
 
 @pytest.mark.parametrize("hd,heads,kvh,shared,fixed", [

@@ -391,35 +391,6 @@ struct DmaShape {
     static_assert((2 * NK) % W == 0 && DPW % 2 == 0 && DPW <= 15, "DMA split");
 };
 
-// Word 3 of a raw buffer resource on gfx950 (32-bit data format, no swizzle).
-constexpr uint32_t kBufferRsrcWord3 = 0x00020000u;
-
-// LDS DMA of 16 bytes per lane: bytes [voff, voff + 16) of the buffer at base
-// (wave-uniform, `bytes` long) to lds + 16 * lane.  The MUBUF form is used
-// rather than global_load_lds: the compiler counts a pending FLAT-encoded LDS
-// DMA against the LDS counter too and then waits for every outstanding LDS
-// read (lgkmcnt(0)) wherever it needs one, while a MUBUF DMA counts only in
-// vmcnt and the ds_read waits stay partial.
-__device__ __forceinline__ void dma16(const void *base, uint32_t bytes, void *lds, uint32_t voff) {
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufferRsrcWord3);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds,
-                                             16, voff, 0, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t uniform_u32(uint32_t x) {
-    return __builtin_amdgcn_readfirstlane(x);
-}
-
-// s_waitcnt vmcnt(N) lgkmcnt(0), then a workgroup barrier.
-template <int N>
-__device__ __forceinline__ void wait_barrier() {
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 __device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
                                           uint32_t i) {
     return i < 2 ? (i == 0 ? a : b) : (i == 2 ? c : d);

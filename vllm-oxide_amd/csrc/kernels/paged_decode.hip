@@ -34,11 +34,14 @@
 // Row packing.  One row's group fills G of the MFMA tile's 16 head columns.
 // When the plan finds full splits of several rows over the same physical
 // blocks (aliased block-table entries: a shared prefix), one work item
-// serves up to 16 / G of them (`pack`; the others are listed in `mates`):
-// column h takes head h % G of row slot h / G.  The blocks are then read
-// once per pack instead of once per row, and since MFMA output columns and
-// the per-column softmax never mix, every row's result is bitwise the one
-// it gets unpacked.
+// serves several of them (`pack`; the others are listed in `mates`), and the
+// blocks are read once per pack instead of once per row.  Either up to 16 / G
+// rows share the tile (column c takes head c % G of row slot c / G), or, in a
+// shared pack (shared_split), the workgroup stages each chunk in LDS once and
+// each of its 4 wavefronts takes 16 / G rows in its own tile.  MFMA output
+// columns and the per-column softmax never mix, and a shared pack keeps the
+// register path's per-wavefront states and merge, so every row's result is
+// bitwise the one it gets unpacked.
 //
 // One 32-key chunk (two 16-key blocks b0, b1) of one wavefront:
 //   Q.K^T: S^T[key, h] = K[key, :] . Q[h, :] with v_mfma_f32_16x16x32_bf16,
@@ -64,7 +67,9 @@
 // Roofline: HBM.  Algorithmic bytes per row = keys * kv_heads * head_dim * 2 B
 // * 2 (K and V) + q and out rows + block-table entries.  The MFMA work is
 // <10% of gfx950's bf16 rate even with 12 of 16 head columns padding.
+#include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "vo_device.hpp"
 #include "vo_kernels.hpp"
@@ -169,18 +174,44 @@ __device__ __forceinline__ void take_new_key(Chunk<HD> &r, uint32_t kc, const ui
     }
 }
 
-// Online-softmax update with one chunk.  `nv` = valid keys of this lane's
-// group (0..8); the last chunk of a split passes tail = true.
+// One chunk of the online softmax, in two parts: the scores (chunk_qk), then
+// the softmax update and P.V (chunk_update).  `nv` = valid keys of this
+// lane's group (0..8); the last chunk of a split passes tail = true, with V
+// already masked.  Every product and sum is rounded on its own (no fused
+// multiply-adds), so that a chunk gets the same bits in every inlined copy:
+// the fusion the compiler chooses otherwise depends on the surrounding code
+// (whether a product has other uses, as in a tail chunk's masking).
 template <int HD>
-__device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 *qv, bool tail, int nv,
-                                              float scale_log2, float &m_run, float &l_run,
-                                              floatx4 *acc) {
-    floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+__device__ __forceinline__ void chunk_qk(const bf16x8 (&ka)[HD / 32], const bf16x8 (&kb)[HD / 32],
+                                         const bf16x8 (&qv)[HD / 32], floatx4 &s0, floatx4 &s1) {
+    s0 = floatx4{0.f, 0.f, 0.f, 0.f};
+    s1 = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < HD / 32; ++kk) {
-        s0 = mfma16x16x32(r.ka[kk], qv[kk], s0);
-        s1 = mfma16x16x32(r.kb[kk], qv[kk], s1);
+        s0 = mfma16x16x32(ka[kk], qv[kk], s0);
+        s1 = mfma16x16x32(kb[kk], qv[kk], s1);
     }
+}
+
+// Keys past the end get p = 0; zero their V too, so whatever the pool holds
+// there cannot turn 0*x into NaN.
+template <int HD>
+__device__ __forceinline__ void mask_tail_v(bf16x8 (&va)[HD / 16], int nv) {
+    u32x4 mask;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+        mask[p] = ((2 * p < nv) ? 0x0000ffffu : 0u) | ((2 * p + 1 < nv) ? 0xffff0000u : 0u);
+#pragma unroll
+    for (int dt = 0; dt < HD / 16; ++dt)
+        va[dt] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, va[dt]) & mask);
+}
+
+template <int HD>
+__device__ __forceinline__ void chunk_update(const floatx4 &s0, const floatx4 &s1,
+                                             const bf16x8 (&va)[HD / 16], bool tail, int nv,
+                                             float scale_log2, float &m_run, float &l_run,
+                                             floatx4 (&acc)[HD / 16]) {
+#pragma clang fp contract(off)
     float sc[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -190,15 +221,6 @@ __device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 *qv, bo
     if (tail) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) sc[i] = (i < nv) ? sc[i] : -INFINITY;
-        // Keys past the end get p = 0; zero their V too, so whatever the pool
-        // holds there cannot turn 0*x into NaN.
-        u32x4 mask;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-            mask[p] = ((2 * p < nv) ? 0x0000ffffu : 0u) | ((2 * p + 1 < nv) ? 0xffff0000u : 0u);
-#pragma unroll
-        for (int dt = 0; dt < HD / 16; ++dt)
-            r.va[dt] = __builtin_bit_cast(bf16x8, __builtin_bit_cast(u32x4, r.va[dt]) & mask);
     }
     float mt = sc[0];
 #pragma unroll
@@ -226,14 +248,285 @@ __device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 *qv, bo
 #pragma unroll
     for (int dt = 0; dt < HD / 16; ++dt) {
         acc[dt] *= alpha;
-        acc[dt] = mfma16x16x32(r.va[dt], pb_lo, acc[dt]);
-        acc[dt] = mfma16x16x32(r.va[dt], pb_hi, acc[dt]);
+        acc[dt] = mfma16x16x32(va[dt], pb_lo, acc[dt]);
+        acc[dt] = mfma16x16x32(va[dt], pb_hi, acc[dt]);
     }
+}
+
+template <int HD>
+__device__ __forceinline__ void compute_chunk(Chunk<HD> &r, const bf16x8 (&qv)[HD / 32], bool tail,
+                                              int nv, float scale_log2, float &m_run, float &l_run,
+                                              floatx4 (&acc)[HD / 16]) {
+    floatx4 s0, s1;
+    chunk_qk<HD>(r.ka, r.kb, qv, s0, s1);
+    if (tail) mask_tail_v<HD>(r.va, nv);
+    chunk_update<HD>(s0, s1, r.va, tail, nv, scale_log2, m_run, l_run, acc);
 }
 
 // Keeps the scheduler from moving instructions across this point: the next
 // chunk's loads are all issued before the current chunk's first wait.
 __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// A shared pack: one full split whose blocks the rows of a pack all read
+// (an aliased prefix), for up to W * (16 / G) rows.  Each wavefront owns one
+// 16-column tile (rows w * 16/G ..) and walks every chunk of the split, so
+// the workgroup reads each K/V byte once for all of its rows instead of once
+// per wavefront.  A chunk (two blocks: K b0, K b1, V b0, V b1, one tile
+// each) is copied into LDS by LDS DMA, 16 bytes per lane from the lane's own
+// global address, through a ring of four stages; the workgroup takes two
+// chunks per barrier while the next two load.  The wavefronts then read their operands from LDS at
+// the positions the register path loads from the pool and run its
+// compute_chunk; chunk c updates state c % W, the state the register path's
+// wavefront c % W keeps, and the W states are merged as that path merges its
+// wavefronts, so every column's result is the register path's, bit for bit.
+//
+// LDS bank spread: within a tile, 16-byte unit x sits at unit swz(x).  K
+// unit x = 64 kk + 4 key + j (dims 8 j.. of 32-dim chunk kk): j ^= 2 (key >>
+// 3) ^ (block & 1), so the 16 lanes of one read phase (keys 0-3 and 8-11 of
+// two blocks) fill 16 distinct 4-bank groups.  V unit x = 2 dim + half:
+// half ^= (dim >> 3) & 1.  Both are involutions on the low bits, so the DMA
+// reads global unit swz(u) into LDS unit u.
+// A shared pack keeps W softmax states per wavefront (W x 32 registers at
+// head_dim 128), and its four stages also hold the register path's merge:
+// exactly 4 wavefronts (with 2 the four-stage loop no longer fits two
+// wavefronts per SIMD).
+constexpr int kSharedWaves = 4;
+
+template <int HD>
+struct SharedStage {
+    static constexpr uint32_t TB = kBS * HD * 2;   // bytes of one (block, KV head) tile
+    static constexpr uint32_t BYTES = 4 * TB;      // K b0, K b1, V b0, V b1
+    __device__ static __forceinline__ uint32_t swz_k(uint32_t x, uint32_t b) {
+        return x ^ (((x >> 5) & 1u) << 1) ^ (b & 1u);
+    }
+    __device__ static __forceinline__ uint32_t swz_v(uint32_t x) { return x ^ ((x >> 4) & 1u); }
+};
+
+template <int HD, int W>
+__device__ __forceinline__ void shared_split(
+    const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
+    uint32_t kvh, uint32_t item, const u32x4 rec, const uint32_t *__restrict__ tables,
+    const uint32_t *__restrict__ row_info, uint32_t split_keys, const uint16_t *__restrict__ q,
+    uint16_t *__restrict__ out, float *__restrict__ part_acc, float *__restrict__ part_ml,
+    uint32_t num_heads, uint32_t group, float scale_log2, const uint32_t *__restrict__ mates,
+    uint32_t pack, uint8_t *__restrict__ st0, uint8_t *__restrict__ st1,
+    uint8_t *__restrict__ st2, uint8_t *__restrict__ st3) {
+#pragma clang fp contract(off)  // the merge below rounds as the register path's does
+    constexpr int KK = HD / 32;
+    constexpr int DT = HD / 16;
+    using S = SharedStage<HD>;
+    constexpr uint32_t kTile = kBS * HD;
+    constexpr int NI = S::BYTES / 1024 / W;  // DMA instructions per wavefront and chunk
+    static_assert(S::BYTES % (1024 * W) == 0 && NI <= 15, "chunk DMA split");
+    constexpr uint32_t KIB_PER_TILE = S::TB / 1024;
+
+    const uint32_t row = uniform_u32(rec[0]);
+    const uint32_t split = uniform_u32(rec[1]);
+    const uint32_t *table = tables + uniform_u32(rec[2]);
+    const uint32_t nchunks = split_keys / kChunk;  // a full split
+    // The split's block ids (at most kMaxSplitKeys / 16 = 256), 64 per
+    // register across the lanes, read before the first DMA; a chunk's two ids
+    // are then v_readlane'd.  (Loads from the table after an LDS DMA would be
+    // vector loads, and every wait for one would also wait for the DMA.)
+    constexpr int TV = kMaxSplitKeys / kBS / 64;
+    const uint32_t nblk = 2 * nchunks;
+    uint32_t tv[TV];
+#pragma unroll
+    for (int k = 0; k < TV; ++k) {
+        const uint32_t i = 64 * k + static_cast<uint32_t>(threadIdx.x & 63);
+        tv[k] = i < nblk ? table[i] : 0u;
+    }
+    auto block_id = [&](uint32_t i) {  // i < nblk, wave-uniform
+        uint32_t b = __builtin_amdgcn_readlane(tv[0], i & 63);
+#pragma unroll
+        for (int k = 1; k < TV; ++k) {
+            const uint32_t bk = __builtin_amdgcn_readlane(tv[k], i & 63);
+            b = (i >> 6) == static_cast<uint32_t>(k) ? bk : b;
+        }
+        return b;
+    };
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane & 15;
+    const int g = lane >> 4;
+
+    // This wavefront's columns: row slot wave * R + h / G, head h % G, with
+    // R = ceil(pack / W) <= 16 / G rows per wavefront.
+    const uint32_t per_wave = (pack + W - 1) / W;
+    const uint32_t hslot = static_cast<uint32_t>(h) / group;
+    const uint32_t pslot = static_cast<uint32_t>(wave) * per_wave + hslot;
+    const uint32_t hh = static_cast<uint32_t>(h) - hslot * group;
+    uint32_t crow = kNoMate;
+    if (hslot < per_wave) {
+        if (pslot == 0)
+            crow = row;
+        else if (pslot < pack)
+            crow = mates[(pack - 1) * item + pslot - 1];
+    }
+    const bool head_ok = crow != kNoMate;
+    // Whether any column of this wavefront is live (wave-uniform).
+    const bool wave_live = __builtin_amdgcn_ballot_w64(head_ok) != 0;
+    const uint32_t qhead = kvh * group + hh;
+    bf16x8 qv[KK];
+    {
+        const uint16_t *qp = q + (static_cast<uint64_t>(head_ok ? crow : row) * num_heads + qhead) * HD + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qv[kk] = head_ok ? load_bf16x8(qp + 32 * kk) : bf16x8{};
+    }
+    u32x2 cinfo = {0u, 0u};
+    if (head_ok) cinfo = *reinterpret_cast<const u32x2 *>(row_info + 2 * static_cast<uint64_t>(crow));
+
+    // DMA: instruction i of wavefront w copies KiB qi = i * W + w of the
+    // stage: tile qi / KIB_PER_TILE (K b0, K b1, V b0, V b1), its KiB qi %
+    // KIB_PER_TILE; lane unit u of that tile reads global unit swz(u).
+    uint32_t dma_off[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const uint32_t qi = static_cast<uint32_t>(i * W + wave);
+        const uint32_t t = qi / KIB_PER_TILE;
+        const uint32_t u = (qi % KIB_PER_TILE) * 64 + lane;
+        dma_off[i] = 16 * (t < 2 ? S::swz_k(u, t) : S::swz_v(u));
+    }
+    const uint64_t block_stride = static_cast<uint64_t>(kv_heads) * kTile;
+    auto dma_chunk = [&](uint8_t *stage, uint32_t c) {
+        const uint32_t b0 = block_id(2 * c);
+        const uint32_t b1 = block_id(2 * c + 1);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t qi = static_cast<uint32_t>(i * W + wave);
+            const uint32_t t = qi / KIB_PER_TILE;
+            const uint16_t *pool = t < 2 ? k_pool : v_pool;
+            const uint32_t blk = (t & 1) ? b1 : b0;
+            dma16(pool + static_cast<uint64_t>(blk) * block_stride + static_cast<uint64_t>(kvh) * kTile,
+                  S::TB, stage + qi * 1024, dma_off[i]);
+        }
+    };
+
+    // LDS read offsets of this lane (the register path's LaneMap positions,
+    // swizzled): K A-row m = l % 16 reads key 8((m >> 2) & 1) + (m & 3) of
+    // block m >= 8, dims 8 g .. of chunk kk (+64 kk units) and the key + 4
+    // (+16 units); V lane reads dim 16 dt + m (+32 dt units), keys 8 (g & 1)
+    // .. +7 of block g >= 2.
+    const uint32_t m = static_cast<uint32_t>(h);
+    const uint32_t kb_hi = m >= 8 ? 1u : 0u;
+    const uint32_t kx = (8 * ((m >> 2) & 1) + (m & 3)) * 4 + static_cast<uint32_t>(g);
+    const uint32_t k_rd = kb_hi * S::TB + 16 * S::swz_k(kx, kb_hi);
+    const uint32_t vb_hi = g >= 2 ? 1u : 0u;
+    const uint32_t vx = 2 * m + static_cast<uint32_t>(g & 1);
+    const uint32_t v_rd = (2 + vb_hi) * S::TB + 16 * S::swz_v(vx);
+
+    // Chunk c goes to state c % W: the (m, l, acc) the register path's
+    // wavefront c % W keeps, in the same order, merged at the end as that
+    // path merges its wavefronts.  So a row's bits do not depend on whether
+    // it was packed.
+    float ms[W], ls[W];
+    floatx4 as[W][DT];
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        ms[w] = -INFINITY;
+        ls[w] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) as[w][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // Chunk c (stage c % 4) updates state c % 4.  Step k takes chunks 2k and
+    // 2k + 1 at once (two independent softmax chains, which the scheduler
+    // interleaves): it waits for them (issued by step k - 1) and for every
+    // wavefront to be done with chunks 2k - 2 and 2k - 1, then refills those
+    // two stages with chunks 2k + 2 and 2k + 3, which load while it computes.
+    auto read_k = [&](const uint8_t *cur, bf16x8 (&ka)[KK], bf16x8 (&kb)[KK])
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            ka[kk] = *reinterpret_cast<const bf16x8 *>(cur + k_rd + 1024 * kk);
+            kb[kk] = *reinterpret_cast<const bf16x8 *>(cur + k_rd + 1024 * kk + 256);
+        }
+    };
+    auto read_v = [&](const uint8_t *cur, bf16x8 (&va)[DT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) va[dt] = *reinterpret_cast<const bf16x8 *>(cur + v_rd + 512 * dt);
+    };
+    auto step = [&](auto half_c, uint32_t c) __attribute__((always_inline)) {
+        constexpr int hf = decltype(half_c)::value;  // 0: stages/states 0, 1; 1: 2, 3
+        uint8_t *__restrict__ ca = hf ? st2 : st0;
+        uint8_t *__restrict__ cb = hf ? st3 : st1;
+        uint8_t *__restrict__ na = hf ? st0 : st2;
+        uint8_t *__restrict__ nb = hf ? st1 : st3;
+        wait_barrier<0>();
+        if (c + 2 < nchunks) dma_chunk(na, c + 2);
+        if (c + 3 < nchunks) dma_chunk(nb, c + 3);
+        if (!wave_live) return;
+        bf16x8 ka[KK], kb[KK], va[DT];
+        floatx4 sa0, sa1;
+        read_k(ca, ka, kb);
+        chunk_qk<HD>(ka, kb, qv, sa0, sa1);
+        if (c + 1 < nchunks) {
+            floatx4 sb0, sb1;
+            read_k(cb, ka, kb);
+            chunk_qk<HD>(ka, kb, qv, sb0, sb1);
+            read_v(ca, va);
+            chunk_update<HD>(sa0, sa1, va, false, 8, scale_log2, ms[2 * hf], ls[2 * hf], as[2 * hf]);
+            read_v(cb, va);
+            chunk_update<HD>(sb0, sb1, va, false, 8, scale_log2, ms[2 * hf + 1], ls[2 * hf + 1],
+                                as[2 * hf + 1]);
+        } else {
+            read_v(ca, va);
+            chunk_update<HD>(sa0, sa1, va, false, 8, scale_log2, ms[2 * hf], ls[2 * hf], as[2 * hf]);
+        }
+    };
+    static_assert(W == 4, "state index = stage index");
+    dma_chunk(st0, 0);
+    if (nchunks > 1) dma_chunk(st1, 1);
+    for (uint32_t c = 0; c < nchunks; c += 4) {
+        step(std::integral_constant<int, 0>{}, c);
+        if (c + 2 >= nchunks) break;
+        step(std::integral_constant<int, 1>{}, c + 2);
+    }
+
+    if (!head_ok) return;
+    // The register path's merge of its W wavefronts, per element.
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        ls[w] += __shfl_xor(ls[w], 16, 64);
+        ls[w] += __shfl_xor(ls[w], 32, 64);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, ms[w]);
+    float den = 0.0f;
+    floatx4 num[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) num[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        const float mw = ms[w];
+        if (mw != -INFINITY) {
+            const float e = __builtin_amdgcn_exp2f(mw - mx);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) num[dt][j] += e * as[w][dt][j];
+            den += e * ls[w];
+        }
+    }
+    if (cinfo[1] == 1) {
+        uint16_t *op = out + static_cast<uint64_t>(crow) * num_heads * HD +
+                       static_cast<uint64_t>(qhead) * HD + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) op[16 * dt + j] = f32_to_bf16_bits(num[dt][j] / den);
+    } else {
+        const uint64_t part = static_cast<uint64_t>(cinfo[0] + split) * num_heads + qhead;
+        float *ap = part_acc + part * HD + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = num[dt];
+        if (g == 0) {
+            part_ml[2 * part] = mx;
+            part_ml[2 * part + 1] = den;
+        }
+    }
+}
 
 template <int HD, int W, bool NT>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void
@@ -246,11 +539,25 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                      uint32_t group, float scale_log2, const uint32_t *__restrict__ counts,
                      const uint32_t *__restrict__ mates, uint32_t pack, uint16_t *__restrict__ k_w,
                      uint16_t *__restrict__ v_w, const uint16_t *__restrict__ new_k,
-                     const uint16_t *__restrict__ new_v, const uint32_t *__restrict__ new_slots) {
+                     const uint16_t *__restrict__ new_v, const uint32_t *__restrict__ new_slots,
+                     uint32_t num_shared) {
+#pragma clang fp contract(off)  // the wavefronts' merge rounds as a shared pack's does
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
     constexpr uint32_t kTile = kBS * HD;
     __shared__ uint32_t s_col[3][16];  // per column: row, first partial, splits
+    extern __shared__ float smem[];  // the wavefronts' merge (without stages)
+    // The stages of a shared pack (four objects of their own, so that the
+    // compiler can tell one stage's DMA from another stage's reads and waits
+    // for neither); the register path's merge keeps wavefront w's
+    // accumulators in stage w.
+    constexpr bool kStages = W == kSharedWaves && !NT;
+    constexpr uint32_t kStageBytes = kStages ? SharedStage<HD>::BYTES : 16;
+    __shared__ __align__(1024) uint8_t sh0[kStageBytes];
+    __shared__ __align__(1024) uint8_t sh1[kStageBytes];
+    __shared__ __align__(1024) uint8_t sh2[kStageBytes];
+    __shared__ __align__(1024) uint8_t sh3[kStageBytes];
+    __shared__ float s_ml[kStages ? 2 * W * 16 : 1];
 
     const uint32_t item = blockIdx.x / kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads;
@@ -272,6 +579,16 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
             out[out_base + static_cast<uint64_t>(kvh) * group * HD + idx] = 0;
         return;
     }
+    if constexpr (kStages) {
+        if (item < num_shared) {
+            shared_split<HD, W>(k_pool, v_pool, kv_heads, kvh, item, rec, tables, row_info,
+                                split_keys, q, out, part_acc, part_ml, num_heads, group,
+                                scale_log2, mates, pack, sh0, sh1, sh2, sh3);
+            return;
+        }
+    }
+    // In a plan with shared packs every item with mates is one of them.
+    if (num_shared != 0) pack = 1;
 
     const uint32_t k_begin = split * split_keys;
     const uint32_t k_end = min(nk, k_begin + split_keys);
@@ -433,11 +750,17 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
         }
     } else {
         // Merge the W wavefronts' (m, l, acc) through LDS.
-        extern __shared__ float smem[];
-        float *sm_m = smem;             // [W][16]
-        float *sm_l = sm_m + W * 16;    // [W][16]
-        float *sm_acc = sm_l + W * 16;  // [W][cols][HD]
+        float *sm_m = kStages ? s_ml : smem;  // [W][16]
+        float *sm_l = sm_m + W * 16;          // [W][16]
+        // [W][cols][HD]: wavefront w's block at sm_acc_w(w)
+        float *sm_acc = kStages ? nullptr : sm_l + W * 16;
         const uint32_t cols = pack * group;
+        auto sm_acc_w = [&](int w) -> float * {
+            if constexpr (kStages)
+                return reinterpret_cast<float *>(w == 0 ? sh0 : (w == 1 ? sh1 : (w == 2 ? sh2 : sh3)));
+            else
+                return sm_acc + static_cast<uint32_t>(w) * cols * HD;
+        };
         if (wave == 0 && g == 0) {
             s_col[0][h] = crow;
             s_col[1][h] = cinfo[0];
@@ -448,7 +771,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                 sm_m[wave * 16 + h] = m_run;
                 sm_l[wave * 16 + h] = l_run;
             }
-            float *ap = sm_acc + (static_cast<uint32_t>(wave) * cols + h) * HD + 4 * g;
+            float *ap = sm_acc_w(wave) + h * HD + 4 * g;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = acc[dt];
         }
@@ -467,7 +790,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                 const float mw = sm_m[w * 16 + col];
                 if (mw != -INFINITY) {
                     const float e = __builtin_amdgcn_exp2f(mw - mx);
-                    num += e * sm_acc[(w * cols + col) * HD + d];
+                    num += e * sm_acc_w(w)[col * HD + d];
                     den += e * sm_l[w * 16 + col];
                 }
             }
@@ -565,8 +888,21 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                         hipStream_t stream, const NewKeys *nkeys) {
     const uint32_t group = num_heads / pool.kv_heads;
     const uint32_t pack = plan.pack ? plan.pack : 1;
-    if (pack * group > 16 || (pack > 1 && plan.mates == nullptr)) return hipErrorInvalidValue;
-    const size_t smem = (W == 1) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * pack * group * HD) * 4;
+    const uint32_t shared = plan.num_shared;
+    // Shared packs: W wavefronts of up to 16 / G rows; the other items then
+    // carry no mates.  (A shared pack never holds a row's new key: its blocks
+    // are read by another row, so a plan with new keys has none there.)
+    if (shared != 0 && (W != kSharedWaves || NT || group > 16 || pack > W * (16 / group) ||
+                        plan.split_keys % kChunk != 0))
+        return hipErrorInvalidValue;
+    const uint32_t item_pack = shared ? 1u : pack;
+    if (item_pack * group > 16 || (pack > 1 && plan.mates == nullptr)) return hipErrorInvalidValue;
+    // With 4 wavefronts (not streaming) the merge lives in the shared-pack
+    // stages (at most 16 columns of HD floats per wavefront, 8 KiB at
+    // head_dim 128).
+    constexpr bool kStages = W == kSharedWaves && !NT;
+    const size_t smem =
+        (W == 1 || kStages) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * item_pack * group * HD) * 4;
     const uint64_t grid = static_cast<uint64_t>(plan.launch_work) * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
@@ -576,7 +912,7 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
                        scale_log2, plan.counts, plan.mates, pack, pool.k, pool.v,
                        nkeys ? nkeys->k : nullptr, nkeys ? nkeys->v : nullptr,
-                       nkeys ? nkeys->slots : nullptr);
+                       nkeys ? nkeys->slots : nullptr, shared);
     return hipGetLastError();
 }
 

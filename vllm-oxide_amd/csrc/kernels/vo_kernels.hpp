@@ -166,10 +166,16 @@ struct DecodePlan {
     uint32_t launch_reduce;       // reduce rows launched (>= num_reduce_rows)
     // Row packing: item i also serves the rows mates[(pack-1)*i .. +pack-2]
     // (kNoMate where its pack is short), rows whose split reads the same
-    // blocks; the pack * group head columns fit one 16-column MFMA tile.
+    // blocks; the pack * group head columns fit one 16-column MFMA tile, or
+    // two (the kernel then runs both tiles on every item).
     // pack == 1: no mates (mates may be null).
     const uint32_t *mates;
     uint32_t pack;
+    // Items 0 .. num_shared - 1 are shared packs (mates over one full split):
+    // the workgroup stages each chunk in LDS once and its W wavefronts take
+    // 16 / group rows each, so pack <= W * (16 / group); every other item
+    // then has no mates.  0: no shared packs.
+    uint32_t num_shared;
 };
 
 constexpr uint32_t kNoMate = 0xffffffffu;

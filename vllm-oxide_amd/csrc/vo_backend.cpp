@@ -356,24 +356,69 @@ bool decode_streaming(vo_step_meta *m) {
 // Rows with zero keys still get one work item (it writes the zero output).
 uint64_t row_splits(uint64_t keys, uint64_t L) { return keys ? (keys + L - 1) / L : 1; }
 
-// Row packing.  The split kernel computes 16 head columns per MFMA, of which
-// one row's KV-head group uses G = query heads / KV heads.  Full splits of
-// different rows that read the same physical blocks (aliased block-table
-// entries: a shared prefix) go to one workgroup, up to 16 / G rows, so those
-// blocks are read once per pack instead of once per row.  Each row keeps its
-// own columns, softmax and partial, so its result is bitwise the one it gets
-// unpacked.  The limit uses the largest group the metadata admits, so any
-// call's group fits; the staging buffer is sized for it.  VO_DECODE_PACK=0
-// turns packing off (decode_pack_factor).
-uint32_t decode_pack_limit(const vo_step_meta *m) {
+// Row packing.  The split kernel computes 16 head columns per MFMA tile, of
+// which one row's KV-head group uses G = query heads / KV heads.  Full splits
+// of different rows that read the same physical blocks (aliased block-table
+// entries: a shared prefix) go to one workgroup, so those blocks are read
+// once per pack instead of once per row.  Each row keeps its own columns,
+// softmax and partial, so its result is bitwise the one it gets unpacked.
+// Modes (VO_DECODE_PACK): 0 off; 1 one tile per item (16 / G rows, the
+// register path); 2 (default) shared packs: the workgroup stages each chunk
+// in LDS once and each of its 4 wavefronts takes one tile, 4 * (16 / G)
+// rows.  The limits use the largest group the metadata admits, so any call's
+// group fits; the staging buffer is sized for the largest
+// (decode_pack_limit).
+enum PackMode : uint32_t { kPackOff = 0, kPackOneTile = 1, kPackShared = 2 };
+
+uint64_t max_group(const vo_step_meta *m) {
+    return std::max<uint64_t>(1, (m->max_heads + m->kv_heads - 1) / m->kv_heads);
+}
+
+// Rows per item with `tiles` 16-column tiles shared by all rows.
+uint32_t decode_pack_rows(const vo_step_meta *m, uint32_t tiles) {
     if (m->kv_heads == 0) return 1;
-    const uint64_t group = std::max<uint64_t>(1, (m->max_heads + m->kv_heads - 1) / m->kv_heads);
-    const uint64_t p = 16 / group;
+    const uint64_t p = 16 * tiles / max_group(m);
     return p >= 2 ? static_cast<uint32_t>(p) : 1u;
 }
 
-uint32_t decode_pack_factor(const vo_step_meta *m) {
-    return env_int("VO_DECODE_PACK", 1) == 0 ? 1u : decode_pack_limit(m);
+// Rows per shared pack: 16 / G per wavefront.
+uint32_t decode_shared_rows(const vo_step_meta *m, uint32_t waves) {
+    if (m->kv_heads == 0) return 1;
+    const uint64_t p = waves * (16 / max_group(m));
+    return p >= 2 ? static_cast<uint32_t>(p) : 1u;
+}
+
+uint32_t decode_pack_limit(const vo_step_meta *m) {
+    return std::max(decode_pack_rows(m, 1), decode_shared_rows(m, 4));
+}
+
+uint32_t decode_pack_mode() {
+    const int v = env_int("VO_DECODE_PACK", kPackShared);
+    return (v <= 0) ? kPackOff : static_cast<uint32_t>(std::min(v, static_cast<int>(kPackShared)));
+}
+
+// Moves the packs of two or more rows (pack_fill >= 2) in front of the rest,
+// keeping order within both; returns their number.  Records hold (row,
+// split) in their first two words; mates rows move along.
+uint64_t shared_packs_first(vo_step_meta *m, uint32_t *work, uint64_t n, uint32_t P,
+                            uint32_t *mates) {
+    std::vector<uint32_t> w(2 * n), mt(static_cast<size_t>(P - 1) * n);
+    uint64_t at = 0, ns = 0;
+    for (int pass = 0; pass < 2; ++pass)
+        for (uint64_t i = 0; i < n; ++i) {
+            if ((m->pack_fill[i] >= 2) != (pass == 0)) continue;
+            w[2 * at] = work[4 * i];
+            w[2 * at + 1] = work[4 * i + 1];
+            std::copy(mates + (P - 1) * i, mates + (P - 1) * (i + 1), mt.begin() + (P - 1) * at);
+            ++at;
+            if (pass == 0) ++ns;
+        }
+    for (uint64_t i = 0; i < n; ++i) {
+        work[4 * i] = w[2 * i];
+        work[4 * i + 1] = w[2 * i + 1];
+    }
+    std::copy(mt.begin(), mt.end(), mates);
+    return ns;
 }
 
 // Packs work[0 .. nfull) (full splits; (row, split) in the first two words
@@ -476,25 +521,56 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     const bool streaming = pk.fixed() ? m->fixed.streaming : decode_streaming(m);
     // Packing needs shared blocks, so a streaming plan never packs; a fixed
     // launch keeps one item per (row, split).
-    const uint32_t P = (pk.fixed() || streaming || L % m->block_size != 0) ? 1u : decode_pack_factor(m);
+    uint32_t mode = (pk.fixed() || streaming || L % m->block_size != 0) ? kPackOff : decode_pack_mode();
+    const int waves = decode_waves();
+    // Shared packs need 4 wavefronts (the kernel keeps one softmax state per
+    // wavefront in registers and stages four chunks).
+    if (mode == kPackShared && waves != 4) mode = kPackOneTile;
+    uint32_t P = mode == kPackOff      ? 1u
+                 : mode == kPackShared ? decode_shared_rows(m, static_cast<uint32_t>(waves))
+                                       : decode_pack_rows(m, 1);
     uint32_t *mates = nullptr;
     m->plan.mates = nullptr;
+    m->plan.num_shared = 0;
     if (P > 1) {
         mates = pk.add(kRegMates, (P - 1) * parts, &dp);
         m->plan.mates = dp;
     }
+    auto full_splits = [&]() {
+        uint64_t nf = 0;
+        for (uint64_t i = 0; i < R; ++i) {
+            const uint64_t r = row_at(i);
+            for (uint64_t sp = 0; sp < m->row_num_keys[r] / L; ++sp, ++nf) {
+                work[4 * nf] = static_cast<uint32_t>(r);
+                work[4 * nf + 1] = static_cast<uint32_t>(sp);
+            }
+        }
+        return nf;
+    };
+    f = full_splits();
     for (uint64_t i = 0; i < R; ++i) {
         const uint64_t r = row_at(i);
         const uint64_t nk = m->row_num_keys[r];
-        for (uint64_t sp = 0; sp < nk / L; ++sp, ++f) {
-            work[4 * f] = static_cast<uint32_t>(r);
-            work[4 * f + 1] = static_cast<uint32_t>(sp);
-        }
         if (nk % L != 0 || nk == 0)
             m->tail_items.push_back({static_cast<uint32_t>(nk % L), static_cast<uint32_t>(r),
                                      static_cast<uint32_t>(nk / L)});
     }
-    if (P > 1) f = pack_full_splits(m, work, f, L, P, mates);
+    if (P > 1) {
+        const uint64_t nfull = f;
+        f = pack_full_splits(m, work, nfull, L, P, mates);
+        if (mode == kPackShared) {
+            // Shared packs first; the other items run as single rows.  With
+            // no pack of two rows there is nothing to share.
+            uint32_t fullest = 0;
+            for (uint32_t fill : m->pack_fill) fullest = std::max(fullest, fill);
+            if (fullest >= 2) {
+                m->plan.num_shared = static_cast<uint32_t>(shared_packs_first(m, work, f, P, mates));
+            } else {
+                P = 1;
+                f = full_splits();
+            }
+        }
+    }
     std::stable_sort(m->tail_items.begin(), m->tail_items.end(),
                      [](const TailItem &a, const TailItem &b) { return a.keys > b.keys; });
     for (const TailItem &t : m->tail_items) {
