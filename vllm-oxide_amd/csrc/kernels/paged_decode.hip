@@ -286,6 +286,11 @@ __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0
 // two blocks) fill 16 distinct 4-bank groups.  V unit x = 2 dim + half:
 // half ^= (dim >> 3) & 1.  Both are involutions on the low bits, so the DMA
 // reads global unit swz(u) into LDS unit u.
+// Floats per column of the wavefronts' merge buffer: 4 more than head_dim, so
+// that the 16 columns of one store phase fall into 16 different bank groups.
+template <int HD>
+constexpr uint32_t kAccStride = HD + 4;
+
 // A shared pack keeps W softmax states per wavefront (W x 32 registers at
 // head_dim 128), and its four stages also hold the register path's merge:
 // exactly 4 wavefronts (with 2 the four-stage loop no longer fits two
@@ -558,6 +563,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     __shared__ __align__(1024) uint8_t sh2[kStageBytes];
     __shared__ __align__(1024) uint8_t sh3[kStageBytes];
     __shared__ float s_ml[kStages ? 2 * W * 16 : 1];
+    static_assert(!kStages || 16 * kAccStride<HD> * 4 <= kStageBytes, "merge fits a stage");
 
     const uint32_t item = blockIdx.x / kv_heads;
     const uint32_t kvh = blockIdx.x % kv_heads;
@@ -759,7 +765,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
             if constexpr (kStages)
                 return reinterpret_cast<float *>(w == 0 ? sh0 : (w == 1 ? sh1 : (w == 2 ? sh2 : sh3)));
             else
-                return sm_acc + static_cast<uint32_t>(w) * cols * HD;
+                return sm_acc + static_cast<uint32_t>(w) * cols * kAccStride<HD>;
         };
         if (wave == 0 && g == 0) {
             s_col[0][h] = crow;
@@ -771,7 +777,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                 sm_m[wave * 16 + h] = m_run;
                 sm_l[wave * 16 + h] = l_run;
             }
-            float *ap = sm_acc_w(wave) + h * HD + 4 * g;
+            float *ap = sm_acc_w(wave) + h * kAccStride<HD> + 4 * g;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = acc[dt];
         }
@@ -790,7 +796,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                 const float mw = sm_m[w * 16 + col];
                 if (mw != -INFINITY) {
                     const float e = __builtin_amdgcn_exp2f(mw - mx);
-                    num += e * sm_acc_w(w)[col * HD + d];
+                    num += e * sm_acc_w(w)[col * kAccStride<HD> + d];
                     den += e * sm_l[w * 16 + col];
                 }
             }
@@ -902,7 +908,8 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
     // head_dim 128).
     constexpr bool kStages = W == kSharedWaves && !NT;
     const size_t smem =
-        (W == 1 || kStages) ? 0 : (2 * W * 16 + static_cast<size_t>(W) * item_pack * group * HD) * 4;
+        (W == 1 || kStages) ? 0
+                            : (2 * W * 16 + static_cast<size_t>(W) * item_pack * group * kAccStride<HD>) * 4;
     const uint64_t grid = static_cast<uint64_t>(plan.launch_work) * pool.kv_heads;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("decode_splitk", stream);
