@@ -11,13 +11,17 @@ tokens and of every block's contents, and after each step checks:
     block, cache index consistent);
   * each table covers its tokens: ceil(tokens / block_size) blocks;
   * an append's slot is slot_of(table, position) (paged.rs:47-52);
-  * a prefix-cache hit only ever hands out a block whose contents equal the
-    prompt's block (no aliasing of different contents);
+  * a prefix-cache hit only ever hands out a block whose whole prefix (its
+    tokens and every token before it, which its KV at layers >= 1 depends
+    on) equals the prompt's, also when block hashes are made to collide on
+    purpose (VO_BM_TEST_UNCHAINED_HASH: a block hashes its own tokens only);
   * copy on write only copies a block another live sequence still uses, into
     a block nobody else uses;
   * blocks no live table references are all available again;
   * a request the pool cannot serve raises CapacityError and changes nothing.
 """
+import os
+
 import numpy as np
 import pytest
 from hypothesis import HealthCheck, settings
@@ -30,13 +34,22 @@ vo = g._load_package()
 
 
 class BlockManagerMachine(RuleBasedStateMachine):
+    unchained = False  # block hashes ignore the prefix (collisions on purpose)
+
     @initialize(num_blocks=st.integers(4, 40), bs=st.sampled_from([1, 2, 4, 16]),
                 caching=st.booleans())
     def setup(self, num_blocks, bs, caching):
-        self.bm = vo.BlockManager(num_blocks, bs, prefix_caching=caching)
+        if self.unchained:
+            os.environ["VO_BM_TEST_UNCHAINED_HASH"] = "1"
+        try:
+            self.bm = vo.BlockManager(num_blocks, bs, prefix_caching=caching)
+        finally:
+            os.environ.pop("VO_BM_TEST_UNCHAINED_HASH", None)
         self.N, self.bs, self.caching = num_blocks, bs, caching
         self.seqs = {}        # seq id -> list of tokens
-        self.content = {}     # block id -> tuple of tokens of a full block (model)
+        # block id -> the tokens up to the end of that full block (model): its
+        # KV depends on all of them
+        self.content = {}
         self.next_id = 0
 
     # -- helpers ----------------------------------------------------------
@@ -52,7 +65,7 @@ class BlockManagerMachine(RuleBasedStateMachine):
     def _record_full_blocks(self, s):
         toks, table = self.seqs[s], self._table(s)
         for i in range(len(toks) // self.bs):
-            self.content[table[i]] = tuple(toks[i * self.bs:(i + 1) * self.bs])
+            self.content[table[i]] = tuple(toks[:(i + 1) * self.bs])
 
     def _snapshot(self):
         return {s: self._table(s) for s in self.seqs}, self.bm.available()
@@ -84,7 +97,7 @@ class BlockManagerMachine(RuleBasedStateMachine):
         assert cached % self.bs == 0 and cached < len(toks)
         table = self._table(sid)
         for i in range(cached // self.bs):
-            assert self.content.get(table[i]) == tuple(toks[i * self.bs:(i + 1) * self.bs])
+            assert self.content.get(table[i]) == tuple(toks[:(i + 1) * self.bs])
         if not self.caching:
             assert cached == 0
         self.seqs[sid] = toks
@@ -152,6 +165,35 @@ TestBlockManagerStateMachine = BlockManagerMachine.TestCase
 TestBlockManagerStateMachine.settings = settings(
     max_examples=150, stateful_step_count=40, deadline=None,
     suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large])
+
+
+class CollidingHashMachine(BlockManagerMachine):
+    unchained = True
+
+
+TestBlockManagerCollidingHashes = CollidingHashMachine.TestCase
+TestBlockManagerCollidingHashes.settings = TestBlockManagerStateMachine.settings
+
+
+def test_prefix_hit_needs_the_same_verified_prefix(monkeypatch):
+    """A cached block is reused only after the very block the lookup accepted
+    before it.  With VO_BM_TEST_UNCHAINED_HASH=1 a block hashes its own tokens
+    only, so block T after prefix A and block T after prefix B collide: the
+    prompt B + T finds sequence 1's T block (computed after A) and must not
+    take it; A + T still hits both blocks."""
+    monkeypatch.setenv("VO_BM_TEST_UNCHAINED_HASH", "1")
+    bm = vo.BlockManager(32, 4)
+    monkeypatch.delenv("VO_BM_TEST_UNCHAINED_HASH")
+    A, B, T = [1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12]
+    assert bm.add_sequence(1, A + T + [0]) == 0
+    assert bm.add_sequence(2, B + [0]) == 0
+    assert bm.add_sequence(3, B + T + [0]) == 4
+    assert bm.block_table(3)[0] == bm.block_table(2)[0]
+    assert bm.block_table(3)[1] != bm.block_table(1)[1]
+    assert bm.add_sequence(4, T + [0]) == 0          # T was cached at position 1, not 0
+    assert bm.add_sequence(5, A + T + [7]) == 8
+    assert list(bm.block_table(5)[:2]) == list(bm.block_table(1)[:2])
+    bm.check()
 
 
 def test_shared_prefix_blocks_and_last_token_block():

@@ -20,15 +20,21 @@
 //    a fork shares (refcount > 1) copies it first: the manager hands the
 //    caller the (source, destination) pair to copy on the device.
 //  - Prefix caching works on full blocks.  Block i of a sequence hashes
-//    (hash of block i-1, its bs token ids) with FNV-1a 64; a hit is accepted
-//    only when the stored token ids are equal too, so a hash collision can
-//    never alias different contents.  A prompt reuses its longest run of
+//    (hash of block i-1, its bs token ids) with FNV-1a 64, which only finds
+//    the candidate: a hit is accepted when the cached block's token ids
+//    equal the prompt's block AND the block was registered right after the
+//    block the lookup accepted for position i-1 (its id, and its generation,
+//    which changes whenever a block is given new contents).  By induction an
+//    accepted run's whole prefix equals the prompt's, so a hash collision
+//    (FNV is not collision-resistant) can only cost a miss, never reuse KV
+//    computed under another prefix.  A prompt reuses its longest run of
 //    cached leading blocks, but never the block holding its last token,
 //    which the step must compute to produce logits.
 //  - Freeing a sequence drops one reference per table entry; a block reaching
 //    refcount 0 goes to the LRU list if it is a hashed full block, else to
 //    the free list.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <list>
 #include <new>
@@ -59,6 +65,9 @@ struct Block {
     uint32_t refcount = 0;
     bool hashed = false;       // a full block registered in the prefix cache
     uint64_t hash = 0;
+    uint64_t gen = 0;          // bumped whenever the block takes new contents
+    uint32_t parent = kNone;   // while hashed: the block before it (kNone at position 0)
+    uint64_t parent_gen = 0;   // and that block's generation then
     std::vector<uint32_t> tokens;  // its bs token ids while hashed
     std::list<uint32_t>::iterator lru_it;
     bool on_lru = false;
@@ -76,6 +85,10 @@ struct Seq {
 struct vo_block_manager {
     uint64_t num_blocks = 0, block_size = 0;
     bool prefix_caching = false;
+    // Test hook (VO_BM_TEST_UNCHAINED_HASH=1 at creation): hash a block's
+    // own tokens only, so that equal blocks after different prefixes
+    // collide on purpose.
+    bool unchained_hash = false;
     std::vector<Block> blocks;
     std::vector<uint32_t> free_list;       // LIFO
     std::list<uint32_t> lru;               // cached-idle blocks, least recently used first
@@ -112,6 +125,7 @@ struct vo_block_manager {
             return kNone;
         }
         blocks[b].refcount = 1;
+        ++blocks[b].gen;
         return b;
     }
 
@@ -139,7 +153,17 @@ struct vo_block_manager {
     }
 
     uint64_t block_hash(uint64_t prev, const uint32_t *toks) const {
+        if (unchained_hash) prev = 0;
         return fnv1a(fnv1a(kFnvOffset, &prev, sizeof(prev)), toks, block_size * sizeof(uint32_t));
+    }
+
+    // Whether cached block b may stand at position i of a prompt whose
+    // blocks 0 .. i-1 were accepted as `hits` and whose block i holds toks.
+    bool accepts(uint32_t b, const std::vector<uint32_t> &hits, const uint32_t *toks) const {
+        const Block &k = blocks[b];
+        if (!std::equal(k.tokens.begin(), k.tokens.end(), toks)) return false;
+        if (hits.empty()) return k.parent == kNone;
+        return k.parent == hits.back() && k.parent_gen == blocks[hits.back()].gen;
     }
 
     // Registers full block i of `s` in the prefix cache (first writer wins).
@@ -153,6 +177,8 @@ struct vo_block_manager {
         if (blocks[b].hashed || cache.count(h)) return;
         blocks[b].hashed = true;
         blocks[b].hash = h;
+        blocks[b].parent = i ? s.table[i - 1] : kNone;
+        blocks[b].parent_gen = i ? blocks[s.table[i - 1]].gen : 0;
         blocks[b].tokens.assign(s.tokens.begin() + i * block_size,
                                 s.tokens.begin() + (i + 1) * block_size);
         cache.emplace(h, b);
@@ -186,6 +212,8 @@ extern "C" int32_t vo_bm_create(uint64_t num_blocks, uint64_t block_size, int32_
     bm->num_blocks = num_blocks;
     bm->block_size = block_size;
     bm->prefix_caching = prefix_caching != 0;
+    const char *unchained = std::getenv("VO_BM_TEST_UNCHAINED_HASH");
+    bm->unchained_hash = unchained && std::string(unchained) == "1";
     bm->blocks.resize(num_blocks);
     bm->free_list.reserve(num_blocks);
     // Hand out low block ids first.
@@ -218,9 +246,7 @@ extern "C" int32_t vo_bm_add_sequence(vo_block_manager *bm, uint64_t seq_id,
         for (uint64_t i = 0; (i + 1) * bs < num_tokens; ++i) {
             const uint64_t h = bm->block_hash(prev, tokens + i * bs);
             auto it = bm->cache.find(h);
-            if (it == bm->cache.end()) break;
-            const Block &k = bm->blocks[it->second];
-            if (!std::equal(k.tokens.begin(), k.tokens.end(), tokens + i * bs)) break;
+            if (it == bm->cache.end() || !bm->accepts(it->second, hits, tokens + i * bs)) break;
             hits.push_back(it->second);
             hit_hashes.push_back(h);
             prev = h;
