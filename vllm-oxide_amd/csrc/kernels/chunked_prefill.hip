@@ -391,11 +391,6 @@ struct DmaShape {
     static_assert((2 * NK) % W == 0 && DPW % 2 == 0 && DPW <= 15, "DMA split");
 };
 
-__device__ __forceinline__ uint32_t pick4(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
-                                          uint32_t i) {
-    return i < 2 ? (i == 0 ? a : b) : (i == 2 ? c : d);
-}
-
 // Occupancy target: two wavefronts per SIMD, except at head_dim 128 with 4
 // wavefronts per workgroup, where the 112 KiB of LDS leaves one workgroup per
 // CU and so one wavefront per SIMD.
@@ -405,7 +400,8 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
     const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
     const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
-    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2, uint32_t fixed_offset) {
+    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2, uint32_t fixed_offset,
+    uint32_t pool_bytes) {
     constexpr int W = G * R;
     constexpr int HALVES = kQT / (kRG * R);
     using D = DmaShape<HD, W>;
@@ -475,19 +471,31 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         const uint32_t U = i < DPW / 2 ? P ^ ((P >> 4) & 3u) : P ^ ((P >> 4) & 1u);
         dma_off[i] = U * 16;
     }
-    auto dma_tile = [&](uint8_t *stage, uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    // K instruction i and V instruction i + NB copy from the same block, so
+    // a wave touches NB blocks of each tile: slot s is block (s W + wave) / IPB
+    // of the tile.  One buffer resource per pool spans the layer from KV head
+    // kvh's first tile on; a block's byte offset goes in the instruction's
+    // scalar offset, so a DMA costs one s_mov to m0 besides the load.
+    constexpr int NB = DPW / 2;
+    const auto k_rsrc = buffer_rsrc(k_pool + kvh * kTile, pool_bytes - kvh * D::BT);
+    const auto v_rsrc = buffer_rsrc(v_pool + kvh * kTile, pool_bytes - kvh * D::BT);
+    const uint32_t blk_stride = kv_heads * D::BT;  // bytes from a block to the next
+    auto dma_tile = [&](uint8_t *stage, const uint32_t (&boff)[NB]) {
 #pragma unroll
         for (int i = 0; i < DPW; ++i) {
-            const bool is_k = i < DPW / 2;
-            const uint32_t qi = (i % (DPW / 2)) * W + wave;
-            const uint32_t blk = pick4(b0, b1, b2, b3, qi / D::IPB);
-            const uint16_t *pool = is_k ? k_pool : v_pool;
-            const uint16_t *tile_src = pool + (static_cast<uint64_t>(blk) * kv_heads + kvh) * kTile;
-            dma16(tile_src, D::BT, stage + (is_k ? 0 : D::KBYTES) + qi * 1024, dma_off[i]);
+            const bool is_k = i < NB;
+            const uint32_t qi = (i % NB) * W + wave;
+            dma16_at(is_k ? k_rsrc : v_rsrc, stage + (is_k ? 0 : D::KBYTES) + qi * 1024, dma_off[i],
+                     boff[i % NB]);
         }
     };
-    auto blk_of = [&](uint32_t t, int b) {
-        return uniform_u32(tbl[min(4 * t + b, nblk - 1)]);
+    // Byte offsets of tile t's blocks in this wave's slots.
+    auto blk_offs = [&](uint32_t t, uint32_t (&boff)[NB]) {
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+            const uint32_t slot = (static_cast<uint32_t>(s) * W + wave) / D::IPB;
+            boff[s] = uniform_u32(tbl[min(4 * t + slot, nblk - 1)]) * blk_stride;
+        }
     };
 
     float m_run = 0.0f;
@@ -506,7 +514,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     const uint32_t k_rd1 = (kp / 16) * D::BT + (kp & 15) * 64 + 16 * ((gl ^ kx) ^ 2);
     const uint32_t v_rd = D::KBYTES + c * 32 + 16 * (gl ^ ((c >> 3) & 1));
 
-    uint32_t n0, n1, n2, n3;  // block ids of tile t + 2 while step t runs
+    uint32_t nxt[NB];  // block offsets of tile t + 2 while step t runs
     // The stage read and the stage filled are passed as restrict pointers, so
     // the compiler knows this step's DMA does not write what it reads (it
     // then inserts no wait for that DMA before the reads).
@@ -518,11 +526,8 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         // to the table's last entry), so that every step has the same number
         // of DMA instructions in flight and the compiler's wait tracking
         // stays exact through the loop.
-        dma_tile(ahead, n0, n1, n2, n3);
-        n0 = blk_of(t + 3, 0);
-        n1 = blk_of(t + 3, 1);
-        n2 = blk_of(t + 3, 2);
-        n3 = blk_of(t + 3, 3);
+        dma_tile(ahead, nxt);
+        blk_offs(t + 3, nxt);
         const uint32_t j0 = t * kKT;
         if (wp_min >= nrows + p_min || j0 > wp_max) goto staged;
         {
@@ -619,12 +624,11 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         l_run = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
-        dma_tile(st0, blk_of(0, 0), blk_of(0, 1), blk_of(0, 2), blk_of(0, 3));
-        dma_tile(st1, blk_of(1, 0), blk_of(1, 1), blk_of(1, 2), blk_of(1, 3));
-        n0 = blk_of(2, 0);
-        n1 = blk_of(2, 1);
-        n2 = blk_of(2, 2);
-        n3 = blk_of(2, 3);
+        blk_offs(0, nxt);
+        dma_tile(st0, nxt);
+        blk_offs(1, nxt);
+        dma_tile(st1, nxt);
+        blk_offs(2, nxt);
         wait_barrier<DPW>();
         step(fixed_c, B0{}, First{}, 0);
         for (uint32_t t = 1; t < n_tiles; t += 3) {
@@ -720,11 +724,13 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
     // has fewer workgroups than CUs anyway (32-row workgroups below).
     constexpr bool dma_shape = HD == 64 || G * R == 8 || (G == 4 && R == 1);
     if constexpr (dma_shape) {
-        if (prefill_use_dma() && plan.max_keys <= kTableLds * kBS) {
+        if (prefill_use_dma() && plan.max_keys <= kTableLds * kBS &&
+            pool.elems != 0 && pool.elems * 2 <= 0xffffffffull) {
             hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
                                dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
                                meta.table_off, meta.tables, plan.work, q, out, num_heads,
-                               scale_log2, prefill_fixed_offset() ? 1u : 0u);
+                               scale_log2, prefill_fixed_offset() ? 1u : 0u,
+                               static_cast<uint32_t>(pool.elems * 2));
             return hipGetLastError();
         }
     }

@@ -88,6 +88,20 @@ __device__ __forceinline__ void dma16(const void *base, uint32_t bytes, void *ld
                                              16, voff, 0, 0, 0);
 }
 
+// A raw buffer resource over `bytes` bytes from base (wave-uniform).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, kBufferRsrcWord3);
+}
+
+// LDS DMA of 16 bytes per lane from bytes [soff + voff, soff + voff + 16) of
+// the buffer rsrc to lds + 16 * lane; soff is wave-uniform (the scalar
+// offset of the instruction), voff per lane.
+__device__ __forceinline__ void dma16_at(__amdgpu_buffer_rsrc_t rsrc, void *lds, uint32_t voff,
+                                         uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)lds,
+                                             16, voff, soff, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t uniform_u32(uint32_t x) {
     return __builtin_amdgcn_readfirstlane(x);
 }

@@ -34,6 +34,7 @@ struct PoolLayer {
     uint32_t kv_heads;
     uint32_t head_dim;
     uint32_t block_size;
+    uint64_t elems = 0;  // elements of the layer's K (and of its V)
 };
 
 // Device metadata of one step (all u32, device pointers).

@@ -179,6 +179,7 @@ struct vo_kv_pool {
         p.kv_heads = static_cast<uint32_t>(layout.kv_heads);
         p.head_dim = static_cast<uint32_t>(layout.head_dim);
         p.block_size = static_cast<uint32_t>(layout.block_size);
+        p.elems = layer_elems;
         return p;
     }
 };
