@@ -531,15 +531,33 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         const uint32_t j0 = t * kKT;
         if (wp_min >= nrows + p_min || j0 > wp_max) goto staged;
         {
+        // K fragments are read four k-steps ahead of their MFMAs (the
+        // scheduling fence keeps the first four reads ahead of every MFMA),
+        // and the tile's V fragments are all read right after the Q.K^T
+        // MFMAs, so they land while the exps run.
+        constexpr int KA = KS < 4 ? KS : 4;
         floatx16 s0 = {}, s1 = {};
+        bf16x8 ka[KS], kb[KS];
+        auto read_k = [&](int kk) __attribute__((always_inline)) {
+            const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
+            ka[kk] = *reinterpret_cast<const bf16x8 *>(tile + off);
+            kb[kk] = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * D::BT);
+        };
+#pragma unroll
+        for (int kk = 0; kk < KA; ++kk) read_k(kk);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) {
-            const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
-            const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(tile + off);
-            const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * D::BT);
-            s0 = mfma32x32x16(a0, qv[kk], s0);
-            s1 = mfma32x32x16(a1, qv[kk], s1);
+            if (kk + KA < KS) read_k(kk + KA);
+            s0 = mfma32x32x16(ka[kk], qv[kk], s0);
+            s1 = mfma32x32x16(kb[kk], qv[kk], s1);
         }
+        bf16x8 vf[4][DT];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                vf[j][dt] = *reinterpret_cast<const bf16x8 *>(tile + v_rd + j * D::BT + dt * 1024);
 
         float sc[32];
 #pragma unroll
@@ -595,9 +613,8 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
             if constexpr (!first) l_run = sum8(pb_hi, l_run);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const bf16x8 a = *reinterpret_cast<const bf16x8 *>(tile + v_rd + j * D::BT + dt * 1024);
-                if constexpr (first) o_acc[dt] = mfma32x32x16(a, pb_lo, o_acc[dt]);
-                o_acc[dt] = mfma32x32x16(a, pb_hi, o_acc[dt]);
+                if constexpr (first) o_acc[dt] = mfma32x32x16(vf[j][dt], pb_lo, o_acc[dt]);
+                o_acc[dt] = mfma32x32x16(vf[j][dt], pb_hi, o_acc[dt]);
             }
         }
         }
