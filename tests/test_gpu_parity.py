@@ -555,6 +555,101 @@ def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, f
     _assert_close(got, want, f"prefill key far above tile-0 max (factor {factor})")
 
 
+def _oracle_renumbered(vo, wl):
+    """The oracle's output for wl with the physical block ids renumbered
+    0, 1, .. in order of first use (aliasing kept): the attention does not
+    depend on which blocks hold the keys, and the oracle's f32 pool then
+    stays small for a workload on a huge device pool."""
+    import copy
+    ids = {}
+    tables = [np.array([ids.setdefault(int(b), len(ids)) for b in t], np.uint32) for t in wl.tables]
+    small = copy.copy(wl)
+    small.tables = tables
+    small.num_blocks = len(ids)
+    bs = wl.block_size
+    if wl.kind == "decode":
+        small.meta = vo.DecodeMeta.new(
+            [vo.DecodeSeq(int(c), t) for c, t in zip(wl.context_lens, tables)], bs)
+    else:
+        small.meta = vo.PrefillMeta.new(
+            [vo.PrefillSeq(int(c), int(n), t) for c, n, t in zip(wl.context_lens, wl.num_new, tables)],
+            bs)
+    return W.oracle_attention(orc, small)
+
+
+# 8 KV heads x 16 keys x head_dim 128 x bf16 = 32 KiB of a layer's K per block:
+# 131,071 blocks keep the layer's K under 4 GiB, 131,080 put it past.
+_BLOCK_BYTES_8x128 = 8 * 16 * 128 * 2
+
+
+@pytest.mark.parametrize("num_blocks", [(1 << 32) // _BLOCK_BYTES_8x128 - 1,
+                                        (1 << 32) // _BLOCK_BYTES_8x128 + 8])
+def test_prefill_pool_at_and_past_4_gib(vo, num_blocks):
+    """The LDS-DMA prefill kernel addresses a block by a 32-bit byte offset
+    into the layer (one buffer resource per pool), so it serves layers of
+    K (and V) under 4 GiB; a larger layer runs the register-staged kernel
+    with 64-bit addresses.  Both, with tables that use the pool's last blocks
+    (offsets just under and past 2^32), match the oracle."""
+    _say(f"prefill on a {num_blocks}-block pool")
+    rng = np.random.default_rng(71)
+    ctx, new = [700, 130, 2000], [64, 100, 33]
+    need = [-(-(c + n) // 16) for c, n in zip(ctx, new)]
+    top = list(range(num_blocks - 1, num_blocks - 1 - need[0], -1))
+    low = list(range(5, 5 + need[1] // 2))
+    high = list(range(num_blocks - 1 - need[0], num_blocks - 1 - need[0] - (need[1] - len(low)), -1))
+    mixed = [b for pair in zip(low, high) for b in pair] + low[len(high):] + high[len(low):]
+    used = set(top) | set(mixed)
+    rest = [int(b) for b in rng.permutation(num_blocks)[:need[2] + len(used)] if int(b) not in used]
+    tables = [top, mixed, rest[:need[2]]]
+    backend = vo.HipBackend(device=0, max_seqs=8, max_rows=W.FILL_ROWS, max_table_entries=1024,
+                            max_query_heads=32)
+    wl = W.build(vo, backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=num_blocks, context_lens=ctx, num_new=new, seed=71,
+                 tables=tables)
+    out = _out(wl, backend)
+    _assert_close(out.float().cpu().numpy(), _oracle_renumbered(vo, wl),
+                  f"prefill on a {num_blocks}-block pool")
+    del wl, out
+    import torch
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("num_blocks", [(1 << 32) // _BLOCK_BYTES_8x128 - 1,
+                                        (1 << 32) // _BLOCK_BYTES_8x128 + 8])
+def test_decode_shared_packs_pool_at_and_past_4_gib(vo, num_blocks):
+    """Decode with shared packs (8 rows on an aliased 4096-key prefix, group
+    8) and a long row, on pools whose last blocks sit just under and past
+    4 GiB of a layer's K: the packs' LDS DMA and the register path both
+    address those blocks right (oracle tolerance)."""
+    _say(f"decode shared packs on a {num_blocks}-block pool")
+    rng = np.random.default_rng(72)
+    shared = 4096
+    ctx = [shared + e for e in (3, 100, 257, 900, 31, 64, 1000, 5)] + [9000]
+    pre = list(range(num_blocks - 1, num_blocks - 1 - shared // 16, -1))
+    nxt = num_blocks - 1 - shared // 16
+    tables = []
+    for c in ctx[:8]:
+        own = -(-(c + 1) // 16) - shared // 16
+        tables.append(pre + list(range(nxt, nxt - own, -1)))
+        nxt -= own
+    long_need = -(-(ctx[8] + 1) // 16)
+    tables.append([int(b) for b in rng.permutation(nxt)[:long_need]])
+    backend = vo.HipBackend(device=0, max_seqs=16, max_rows=W.FILL_ROWS, max_table_entries=4096,
+                            max_query_heads=64)
+    wl = W.build(vo, backend, kind="decode", heads=64, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=num_blocks, context_lens=ctx, seed=72,
+                 shared_prefix=shared, shared_count=8, tables=tables)
+    out = _out(wl, backend)
+    # 8 rows x 3 splits + 5 for the long row; the 8 rows' two prefix splits
+    # run as one shared pack each.
+    assert backend.step_meta(wl.pool).decode_plan() == (29 - 2 * 7, 29, 8)
+    _assert_close(out.float().cpu().numpy(), _oracle_renumbered(vo, wl),
+                  f"decode shared packs on a {num_blocks}-block pool")
+    del wl, out
+    import torch
+    torch.cuda.empty_cache()
+
+
 def test_prefill_cfg3_full_size_sampled_rows(vo, gpu_backend):
     """8 seqs x 512-row chunks on context U[0, 8192]; every
     row is computed on the GPU, a sample of rows by the oracle."""

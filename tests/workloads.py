@@ -108,10 +108,12 @@ def _randn(torch, shape, gen, device):
 
 def build(vo, backend, *, kind, heads, kv_heads, head_dim, block_size, num_blocks,
           context_lens, num_new=None, seed=0, layer=0, num_layers=1, shared_prefix=0,
-          shared_count=0, extra_blocks=0, keep_host=True, device=0, fill_layers=None):
+          shared_count=0, extra_blocks=0, keep_host=True, device=0, fill_layers=None,
+          tables=None):
     """Build a workload on ``backend`` (a vo.HipBackend).  ``fill_layers``
     (default: just ``layer``) lists the pool layers that receive the same
-    cached context and new tokens."""
+    cached context and new tokens.  ``tables`` (default: disjoint tables from
+    a seeded permutation of the pool) gives each sequence's block ids."""
     fill_layers = [layer] if fill_layers is None else list(fill_layers)
     import torch
     dev = f"cuda:{device}"
@@ -126,7 +128,12 @@ def build(vo, backend, *, kind, heads, kv_heads, head_dim, block_size, num_block
     totals = context_lens + num_new
     nblocks = [int(-(-int(t) // block_size)) + extra_blocks for t in totals]
     shared_blocks = shared_prefix // block_size
-    tables = split_tables(rng, nblocks, num_blocks, shared_blocks, shared_count)
+    if tables is None:
+        tables = split_tables(rng, nblocks, num_blocks, shared_blocks, shared_count)
+    else:
+        tables = [np.asarray(t, dtype=np.uint32) for t in tables]
+        if any(len(t) < nb for t, nb in zip(tables, nblocks)) or len(tables) != S:
+            raise ValueError("a table is shorter than its sequence")
 
     layout = vo.KvLayout(num_layers, num_blocks, block_size, kv_heads, head_dim)
     pool = backend.alloc_kv_pool(layout)
