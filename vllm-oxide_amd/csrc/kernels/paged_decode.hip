@@ -273,8 +273,8 @@ __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0
 // the workgroup reads each K/V byte once for all of its rows instead of once
 // per wavefront.  A chunk (two blocks: K b0, K b1, V b0, V b1, one tile
 // each) is copied into LDS by LDS DMA, 16 bytes per lane from the lane's own
-// global address, through a ring of four stages; the workgroup takes two
-// chunks per barrier while the next two load.  The wavefronts then read their operands from LDS at
+// global address, through a ring of four stages; the workgroup takes one
+// chunk per barrier while the next three load.  The wavefronts then read their operands from LDS at
 // the positions the register path loads from the pool and run its
 // compute_chunk; chunk c updates state c % W, the state the register path's
 // wavefront c % W keeps, and the W states are merged as that path merges its
@@ -434,11 +434,7 @@ __device__ __forceinline__ void shared_split(
         for (int dt = 0; dt < DT; ++dt) as[w][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Chunk c (stage c % 4) updates state c % 4.  Step k takes chunks 2k and
-    // 2k + 1 at once (two independent softmax chains, which the scheduler
-    // interleaves): it waits for them (issued by step k - 1) and for every
-    // wavefront to be done with chunks 2k - 2 and 2k - 1, then refills those
-    // two stages with chunks 2k + 2 and 2k + 3, which load while it computes.
+    // Chunk c (stage c % 4) updates state c % 4.
     auto read_k = [&](const uint8_t *cur, bf16x8 (&ka)[KK], bf16x8 (&kb)[KK])
         __attribute__((always_inline)) {
 #pragma unroll
@@ -451,42 +447,41 @@ __device__ __forceinline__ void shared_split(
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) va[dt] = *reinterpret_cast<const bf16x8 *>(cur + v_rd + 512 * dt);
     };
-    auto step = [&](auto half_c, uint32_t c) __attribute__((always_inline)) {
-        constexpr int hf = decltype(half_c)::value;  // 0: stages/states 0, 1; 1: 2, 3
-        uint8_t *__restrict__ ca = hf ? st2 : st0;
-        uint8_t *__restrict__ cb = hf ? st3 : st1;
-        uint8_t *__restrict__ na = hf ? st0 : st2;
-        uint8_t *__restrict__ nb = hf ? st1 : st3;
-        wait_barrier<0>();
-        if (c + 2 < nchunks) dma_chunk(na, c + 2);
-        if (c + 3 < nchunks) dma_chunk(nb, c + 3);
+    // One chunk per step: step c waits for chunk c (the DMA of chunks c + 1
+    // and c + 2 may fly on) and for every wavefront to be done with chunk
+    // c - 1, refills that stage with chunk c + 3 and computes chunk c into
+    // state c % 4.  Every step issues its DMA (past the last chunk the block
+    // ids repeat the split's last blocks), so the wait count stays uniform.
+    auto one = [&](auto s_c, uint32_t c) __attribute__((always_inline)) {
+        constexpr int sidx = decltype(s_c)::value;
+        uint8_t *__restrict__ cur = sidx == 0 ? st0 : sidx == 1 ? st1 : sidx == 2 ? st2 : st3;
+        uint8_t *__restrict__ nxt = sidx == 0 ? st3 : sidx == 1 ? st0 : sidx == 2 ? st1 : st2;
+        wait_barrier<2 * NI>();
+        dma_chunk(nxt, min(c + 3, nchunks - 1));
         if (!wave_live) return;
         bf16x8 ka[KK], kb[KK], va[DT];
         floatx4 sa0, sa1;
-        read_k(ca, ka, kb);
+        read_k(cur, ka, kb);
         chunk_qk<HD>(ka, kb, qv, sa0, sa1);
-        if (c + 1 < nchunks) {
-            floatx4 sb0, sb1;
-            read_k(cb, ka, kb);
-            chunk_qk<HD>(ka, kb, qv, sb0, sb1);
-            read_v(ca, va);
-            chunk_update<HD>(sa0, sa1, va, false, 8, scale_log2, ms[2 * hf], ls[2 * hf], as[2 * hf]);
-            read_v(cb, va);
-            chunk_update<HD>(sb0, sb1, va, false, 8, scale_log2, ms[2 * hf + 1], ls[2 * hf + 1],
-                                as[2 * hf + 1]);
-        } else {
-            read_v(ca, va);
-            chunk_update<HD>(sa0, sa1, va, false, 8, scale_log2, ms[2 * hf], ls[2 * hf], as[2 * hf]);
-        }
+        read_v(cur, va);
+        chunk_update<HD>(sa0, sa1, va, false, 8, scale_log2, ms[sidx], ls[sidx], as[sidx]);
     };
     static_assert(W == 4, "state index = stage index");
     dma_chunk(st0, 0);
-    if (nchunks > 1) dma_chunk(st1, 1);
+    dma_chunk(st1, min(1u, nchunks - 1));
+    dma_chunk(st2, min(2u, nchunks - 1));
     for (uint32_t c = 0; c < nchunks; c += 4) {
-        step(std::integral_constant<int, 0>{}, c);
+        one(std::integral_constant<int, 0>{}, c);
+        if (c + 1 >= nchunks) break;
+        one(std::integral_constant<int, 1>{}, c + 1);
         if (c + 2 >= nchunks) break;
-        step(std::integral_constant<int, 1>{}, c + 2);
+        one(std::integral_constant<int, 2>{}, c + 2);
+        if (c + 3 >= nchunks) break;
+        one(std::integral_constant<int, 3>{}, c + 3);
     }
+    // The DMA past the last chunk must land before the workgroup's LDS is
+    // released.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 
     if (!head_ok) return;
     // The register path's merge of its W wavefronts, per element.
