@@ -704,7 +704,7 @@ def nested_record(line):
     """The fields of a config's own line that the headline line nests."""
     keep = ("metric", "value", "unit", "ms_per_step", "pct_of_hbm_peak", "tokens_per_s",
             "kernels_us", "roofline", "cpu_baseline", "algorithmic_bytes_per_step",
-            "unique_bytes_per_step")
+            "unique_bytes_per_step", "steps", "warmup", "settle")
     out = {k: line[k] for k in keep if k in line}
     out["workload"] = line["config"]["workload"]
     return out
