@@ -683,21 +683,52 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     }
     wait_barrier<0>();
     if (uniform_u32(redo) != 0) pass(std::false_type{});
+    // Every wave's DMA has landed and its stage reads are done: the stages
+    // can hold the output.
+    wait_barrier<0>();
 
-    if (!row_ok) return;
-    const float inv = 1.0f / l_run;
-    uint16_t *op = out + (static_cast<uint64_t>(row_begin + lr) * num_heads + qhead) * HD + 4 * gl;
+    // The output goes out through LDS.  A wave's MFMA results put 8 dims of
+    // one row in a lane pair, so direct stores would write 16-byte pieces of
+    // 32 rows per instruction; the workgroup's rows hold its G heads side by
+    // side in memory (G * HD * 2 contiguous bytes per row), so staged in LDS
+    // each store instruction writes whole rows.  Wave w's 32 x HD tile sits
+    // in stage w / WPS, 16-byte chunk q of row c at chunk q ^ (c % CH) (no
+    // bank conflicts on the writes).
+    constexpr int ROWB = HD * 2;         // bytes of one (row, head)
+    constexpr int CH = HD / 8;           // 16-byte chunks of one (row, head)
+    constexpr int WTILE = kRG * ROWB;    // one wave's output tile
+    constexpr int WPS = D::STAGE / WTILE;
+    static_assert(W <= 2 * WPS, "the output tiles fit two stages");
+    {
+        const float inv = 1.0f / l_run;
+        uint8_t *tile = (wave < WPS ? st0 : st1) + (wave % WPS) * WTILE + c * ROWB + 8 * gl;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+        for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-            u32x2 packed;
-            packed[0] = f32_to_bf16_bits(o_acc[dt][4 * r4] * inv) |
-                        (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[dt][4 * r4 + 1] * inv)) << 16);
-            packed[1] = f32_to_bf16_bits(o_acc[dt][4 * r4 + 2] * inv) |
-                        (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[dt][4 * r4 + 3] * inv)) << 16);
-            *reinterpret_cast<u32x2 *>(op + 32 * dt + 8 * r4) = packed;
+            for (int r4 = 0; r4 < 4; ++r4) {
+                u32x2 packed;
+                packed[0] = f32_to_bf16_bits(o_acc[dt][4 * r4] * inv) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[dt][4 * r4 + 1] * inv)) << 16);
+                packed[1] = f32_to_bf16_bits(o_acc[dt][4 * r4 + 2] * inv) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[dt][4 * r4 + 3] * inv)) << 16);
+                const uint32_t q4 = static_cast<uint32_t>(4 * dt + r4) ^ (c % CH);
+                *reinterpret_cast<u32x2 *>(tile + 16 * q4) = packed;
+            }
         }
+    }
+    wait_barrier<0>();
+    constexpr uint32_t kRowChunks = G * CH;  // 16-byte chunks of a row's G heads
+    uint16_t *obase = out + (static_cast<uint64_t>(row_begin) * num_heads + kvh * G) * HD;
+    for (uint32_t k = tid; k < nrows * kRowChunks; k += 64 * W) {
+        const uint32_t row = k / kRowChunks;
+        const uint32_t h = (k % kRowChunks) / CH;
+        const uint32_t q4 = k % CH;
+        const uint32_t w = h + G * (row / kRG);
+        const uint32_t cr = row % kRG;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>((w < WPS ? st0 : st1) + (w % WPS) * WTILE +
+                                                         cr * ROWB + 16 * (q4 ^ (cr % CH)));
+        *reinterpret_cast<u32x4 *>(obase + static_cast<uint64_t>(row) * num_heads * HD + h * HD +
+                                   8 * q4) = v;
     }
 }
 
