@@ -555,6 +555,62 @@ def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, f
     _assert_close(got, want, f"prefill key far above tile-0 max (factor {factor})")
 
 
+@pytest.mark.parametrize("with_long", [False, True])
+def test_prefill_batch_invariance_bitwise(vo, gpu_backend, with_long):
+    """A sequence's prefill rows are bitwise the same alone and in a batch
+    (the reference's batch invariance, CLAUDE.md; model.rs:539-584), where
+    the batch changes how the kernels are launched:
+    - alone, sequence A (100 rows: two items) has fewer items x KV heads
+      than CUs and runs in 32-row workgroups; in the batch (with B's 32
+      items) it runs in 64-row workgroups.  Key 200 of A is set to 4 x the
+      head-0 query of A's row 40, ~65 log2 units above that row's other
+      scores (and ~17 at most for the other rows), which puts that row's sum
+      past the fixed offset's range, so row group 1 of A's first item is
+      recomputed with the running max while group 0 keeps the fixed offset,
+      in both;
+    - with_long adds C, whose rows see more keys than the DMA kernel's LDS
+      block table holds: C's item runs on the register-staged kernel, A's
+      and B's items on the DMA kernel, in the batch as alone.
+    A and C also match the oracle (C: sampled rows; its 65,600 cached keys
+    are the only test of that path)."""
+    import torch
+    _say(f"prefill batch invariance (long sequence {with_long})")
+    ctx, new = [300, 500], [100, 2048]
+    if with_long:
+        ctx.append(4096 * 16 + 64)  # past the DMA kernel's 4096-block LDS table
+        new.append(40)
+    num_blocks = sum(-(-(c + n) // 16) for c, n in zip(ctx, new)) + 8
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=num_blocks, context_lens=ctx, num_new=new, seed=71)
+    q40 = wl.q[40, :128].float()
+    keys = wl.ctx_kv[0][0].clone()
+    keys[200, :128] = (4.0 * q40).to(torch.bfloat16)
+    slot = int(wl.tables[0][200 // 16]) * 16 + 200 % 16
+    gpu_backend.write_kv(wl.pool, 0, keys[200:201].contiguous(),
+                         wl.ctx_kv[0][1][200:201].contiguous(), [slot])
+    wl.ctx_kv[0] = (keys, wl.ctx_kv[0][1])
+    wl.host["ctx"][0] = (keys.float().cpu().numpy(), wl.host["ctx"][0][1])
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    items = [-(-n // 64) for n in new]
+    assert items[0] * 8 < cus <= sum(items) * 8, "A alone narrow, the batch wide"
+
+    full = _out(wl, gpu_backend)
+    starts = np.concatenate([[0], np.cumsum(new)])
+    checked = [0, 2] if with_long else [0]
+    for s in checked:
+        a, b = int(starts[s]), int(starts[s + 1])
+        meta1 = vo.PrefillMeta.new([vo.PrefillSeq(int(ctx[s]), int(new[s]), wl.tables[s])], 16)
+        one = gpu_backend.prefill_attention(wl.q[a:b].contiguous(), wl.pool, 0, meta1)
+        assert np.array_equal(_bits(one), _bits(full[a:b])), f"sequence {s}"
+    rows = list(range(100))
+    if with_long:
+        c0 = int(starts[2])
+        rows += [c0, c0 + 17, c0 + 39]
+    got = full.float().cpu().numpy()[rows]
+    assert np.isfinite(got).all()
+    _assert_close(got, W.oracle_attention(orc, wl, rows=rows), "prefill batch invariance rows")
+
+
 def _oracle_renumbered(vo, wl):
     """The oracle's output for wl with the physical block ids renumbered
     0, 1, .. in order of first use (aliasing kept): the attention does not

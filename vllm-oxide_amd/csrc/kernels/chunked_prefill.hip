@@ -414,7 +414,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     __shared__ __align__(1024) uint8_t st0[D::STAGE];
     __shared__ __align__(1024) uint8_t st1[D::STAGE];
     __shared__ __align__(1024) uint8_t st2[D::STAGE];
-    __shared__ uint32_t redo;  // set when a row of the fixed-offset pass left its range
+    __shared__ uint32_t redo;  // bit g: a row of row group g left the fixed-offset range
 
     const uint32_t kvh = blockIdx.x % kv_heads;
     const uint32_t rest = blockIdx.x / kv_heads;
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     const uint32_t seq = work[4 * item + 3];
     const uint32_t p_max = p_min + nrows - 1;
     const uint32_t n_tiles = p_max / kKT + 1;
-    const uint32_t nblk = p_max / kBS + 1;  // <= kTableLds (checked by the launcher)
+    const uint32_t nblk = p_max / kBS + 1;  // <= kTableLds (longer items run on the register kernel)
     const uint32_t *table = tables + table_off[seq];
 
     const uint32_t tid = threadIdx.x;
@@ -515,6 +515,9 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     const uint32_t v_rd = D::KBYTES + c * 32 + 16 * (gl ^ ((c >> 3) & 1));
 
     uint32_t nxt[NB];  // block offsets of tile t + 2 while step t runs
+    // A wave that is not live in the second pass issues its share of the DMA
+    // and meets every barrier, but computes nothing and keeps its state.
+    bool live = true;
     // The stage read and the stage filled are passed as restrict pointers, so
     // the compiler knows this step's DMA does not write what it reads (it
     // then inserts no wait for that DMA before the reads).
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         dma_tile(ahead, nxt);
         blk_offs(t + 3, nxt);
         const uint32_t j0 = t * kKT;
-        if (wp_min >= nrows + p_min || j0 > wp_max) goto staged;
+        if ((!fixed && !live) || wp_min >= nrows + p_min || j0 > wp_max) goto staged;
         {
         // K fragments are read four k-steps ahead of their MFMAs (the
         // scheduling fence keeps the first four reads ahead of every MFMA),
@@ -635,12 +638,16 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     using First = std::integral_constant<bool, true>;
     using Rest = std::integral_constant<bool, false>;
 
-    // One pass over the item's KV tiles; m_run, l_run and o_acc start afresh.
+    // One pass over the item's KV tiles; a live wave's m_run, l_run and
+    // o_acc start afresh.
     auto pass = [&](auto fixed_c) __attribute__((always_inline)) {
-        m_run = 0.0f;
-        l_run = 0.0f;
+        constexpr bool fixed = decltype(fixed_c)::value;  // the first pass: every wave live
+        if (fixed || live) {
+            m_run = 0.0f;
+            l_run = 0.0f;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
+            for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
+        }
         blk_offs(0, nxt);
         dma_tile(st0, nxt);
         blk_offs(1, nxt);
@@ -658,7 +665,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         // The DMA of the tiles past the end is still in flight: it must land
         // before the stages are refilled or the workgroup's LDS is released.
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-        l_run += __shfl_xor(l_run, 32, 64);
+        if (fixed || live) l_run += __shfl_xor(l_run, 32, 64);
     };
 
     // Fixed softmax offset: m_run stays at the row's tile-0 max.  A later
@@ -666,10 +673,14 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     // hold with the same relative precision, and O / l does not depend on
     // the offset; so later tiles need neither a row max nor a rescale.  Only
     // the range can fail: every P is a term of l, and |O| <= l max |V|, so a
-    // row with l below kOverflowSum and a finite O lost nothing.  If any row
-    // of the workgroup is past that, the workgroup recomputes its item with
-    // the running max (raised by more than kLazyLog2 at a time) and writes
-    // that result instead.
+    // row with l below kOverflowSum and a finite O lost nothing.  If a row of
+    // a 32-row group is past that, the group's rows are recomputed with the
+    // running max (raised by more than kLazyLog2 at a time, per wave) in a
+    // second pass, in which the waves of the other groups stay idle and keep
+    // their first-pass results.  The decision is per row group, never per
+    // workgroup, so a row's result does not depend on whether its group
+    // shares a workgroup with the item's other group (which a plan of few
+    // items avoids): the same rows give the same bits in any batch.
     if (fixed_offset) {
         pass(std::true_type{});
         bool ok = l_run < kOverflowSum;  // false for inf and NaN too
@@ -677,12 +688,16 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) ok = ok && __builtin_isfinite(o_acc[dt][r]);
-        if (__builtin_amdgcn_ballot_w64(row_ok && !ok) != 0 && lane == 0) redo = 1u;
+        if (__builtin_amdgcn_ballot_w64(row_ok && !ok) != 0 && lane == 0) atomicOr(&redo, 1u << rg);
     } else if (tid == 0) {
-        redo = 1u;
+        redo = (1u << R) - 1;
     }
     wait_barrier<0>();
-    if (uniform_u32(redo) != 0) pass(std::false_type{});
+    const uint32_t again = uniform_u32(redo);
+    if (again != 0) {
+        live = ((again >> rg) & 1u) != 0;
+        pass(std::false_type{});
+    }
     // Every wave's DMA has landed and its stage reads are done: the stages
     // can hold the output.
     wait_barrier<0>();
@@ -764,28 +779,39 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
                      hipStream_t stream) {
     constexpr int HALVES = kQT / (kRG * R);
     const uint64_t grid = static_cast<uint64_t>(plan.num_items) * HALVES * pool.kv_heads;
-    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
+    if (grid > 0x7fffffffull || plan.num_long > plan.num_items) return hipErrorInvalidValue;
     KernelTimer timer("prefill_mfma", stream);
     // The DMA kernel stages a sequence's whole block table in LDS, and its
     // three 32 KiB stages at head_dim 128 leave room for one workgroup per
     // CU, which takes 8 wavefronts to fill the SIMDs -- or 4 when the grid
-    // has fewer workgroups than CUs anyway (32-row workgroups below).
+    // has fewer workgroups than CUs anyway (32-row workgroups below).  Its
+    // items are those past the plan's num_long; the others (rows past its
+    // table) run on the register-staged kernel, launched first.
+    uint32_t regs_items = plan.num_items;
     constexpr bool dma_shape = HD == 64 || G * R == 8 || (G == 4 && R == 1);
     if constexpr (dma_shape) {
-        if (prefill_use_dma() && plan.max_keys <= kTableLds * kBS &&
-            pool.elems != 0 && pool.elems * 2 <= 0xffffffffull) {
-            hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
-                               dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
-                               meta.table_off, meta.tables, plan.work, q, out, num_heads,
+        if (prefill_use_dma() && pool.elems != 0 && pool.elems * 2 <= 0xffffffffull)
+            regs_items = plan.num_long;
+    }
+    const uint32_t per_item = HALVES * pool.kv_heads;
+    if (regs_items != 0) {
+        hipLaunchKernelGGL((prefill_mfma_kernel<HD, G, R>), dim3(regs_items * per_item),
+                           dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
+                           meta.table_off, meta.tables, plan.work, q, out, num_heads, scale_log2);
+        if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
+    }
+    if constexpr (dma_shape) {
+        if (regs_items < plan.num_items) {
+            hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>),
+                               dim3((plan.num_items - regs_items) * per_item), dim3(64 * G * R), 0,
+                               stream, pool.k, pool.v, pool.kv_heads, meta.table_off, meta.tables,
+                               plan.work + 4 * static_cast<uint64_t>(regs_items), q, out, num_heads,
                                scale_log2, prefill_fixed_offset() ? 1u : 0u,
                                static_cast<uint32_t>(pool.elems * 2));
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((prefill_mfma_kernel<HD, G, R>), dim3(static_cast<uint32_t>(grid)),
-                       dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
-                       meta.tables, plan.work, q, out, num_heads, scale_log2);
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 template <int HD, int G>
@@ -826,6 +852,8 @@ bool prefill_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t gro
 }
 
 uint32_t prefill_rows_per_tile() { return kQT; }
+
+uint32_t prefill_dma_max_keys() { return kTableLds * kBS; }
 
 hipError_t launch_prefill_mfma(const PoolLayer &pool, const MetaView &meta,
                                const PrefillPlan &plan, const uint16_t *q, uint16_t *out,

@@ -211,7 +211,16 @@ struct PrefillPlan {
     const uint32_t *work;  // [num_items][4]: (first row, rows, position of first row, sequence)
     uint32_t num_items;
     uint32_t max_keys;     // largest key count of any row (position + 1) in the plan
+    // Items 0 .. num_long - 1 have rows past prefill_dma_max_keys() keys (the
+    // order is longest first, so they lead); they run on the register-staged
+    // kernel, the others on the DMA kernel.  The choice is made per item, from
+    // the item's own rows, so a sequence's result does not depend on the
+    // other sequences of the batch.
+    uint32_t num_long = 0;
 };
+
+// Keys the DMA prefill kernel takes per row (its block table lives in LDS).
+uint32_t prefill_dma_max_keys();
 
 // True when the MFMA prefill kernel covers this shape.
 bool prefill_mfma_supported(uint32_t head_dim, uint32_t block_size, uint32_t group);

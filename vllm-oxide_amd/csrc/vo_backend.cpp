@@ -657,7 +657,9 @@ vo_status plan_decode(vo_step_meta *m, Packer &pk) { return plan_decode_rows(m, 
 // bitwise the one decode_attention returns; sequences with more rows become
 // 64-row items of the MFMA prefill kernel, sorted by KV tiles, longest first,
 // so that the long ones are scheduled early.  Both kernels cover the same
-// shapes, and each row is written by exactly one of them.
+// shapes, and each row is written by exactly one of them.  Items with rows
+// past prefill_dma_max_keys() keys (a multiple of 64, so exactly the items of
+// more tiles than that / 64) lead the order and are counted in num_long.
 vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens,
                        const uint64_t *seq_row_starts) {
     m->prefill_planned = false;
@@ -704,9 +706,13 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
     }
     m->prefill_plan.work = dp;
     m->prefill_plan.num_items = static_cast<uint32_t>(items.size());
-    uint32_t max_keys = 0;
-    for (const Item &it : items) max_keys = std::max(max_keys, it.pos + it.rows);
+    uint32_t max_keys = 0, num_long = 0;
+    for (const Item &it : items) {
+        max_keys = std::max(max_keys, it.pos + it.rows);
+        num_long += it.pos + it.rows > kernels::prefill_dma_max_keys();
+    }
     m->prefill_plan.max_keys = max_keys;
+    m->prefill_plan.num_long = num_long;
     if (!m->decode_rows.empty())
         if (vo_status rc = plan_decode_rows(m, pk, &m->decode_rows)) return rc;
     m->prefill_planned = true;
