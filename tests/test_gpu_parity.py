@@ -611,6 +611,31 @@ def test_prefill_batch_invariance_bitwise(vo, gpu_backend, with_long):
     _assert_close(got, W.oracle_attention(orc, wl, rows=rows), "prefill batch invariance rows")
 
 
+@pytest.mark.parametrize("hd,heads,kvh", [(64, 32, 8), (128, 16, 8), (128, 64, 8), (64, 8, 4)])
+def test_prefill_batch_invariance_bitwise_shapes(vo, gpu_backend, hd, heads, kvh):
+    """The batch invariance above at the other prefill kernel instances:
+    head_dim 64 with GQA 4 (DMA kernel, 32- or 64-row workgroups), GQA 2
+    (head_dim 128: register-staged kernel; head_dim 64: DMA kernel) and
+    GQA 8 (one row group per workgroup), with the same planted key."""
+    import torch
+    _say(f"prefill batch invariance hd {hd} heads {heads}/{kvh}")
+    ctx, new = [300, 500], [100, 2048]  # alone: 2 items; in the batch: 34 (x KV heads >= CUs at kvh 8)
+    num_blocks = sum(-(-(c + n) // 16) for c, n in zip(ctx, new)) + 8
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=heads, kv_heads=kvh, head_dim=hd,
+                 block_size=16, num_blocks=num_blocks, context_lens=ctx, num_new=new, seed=72,
+                 keep_host=False)
+    keys = wl.ctx_kv[0][0].clone()
+    keys[200, :hd] = (4.0 * wl.q[40, :hd].float()).to(torch.bfloat16)
+    slot = int(wl.tables[0][200 // 16]) * 16 + 200 % 16
+    gpu_backend.write_kv(wl.pool, 0, keys[200:201].contiguous(),
+                         wl.ctx_kv[0][1][200:201].contiguous(), [slot])
+    full = _out(wl, gpu_backend)
+    meta1 = vo.PrefillMeta.new([vo.PrefillSeq(ctx[0], new[0], wl.tables[0])], 16)
+    one = gpu_backend.prefill_attention(wl.q[:new[0]].contiguous(), wl.pool, 0, meta1)
+    assert np.isfinite(one.float().cpu().numpy()).all()
+    assert np.array_equal(_bits(one), _bits(full[:new[0]]))
+
+
 def _oracle_renumbered(vo, wl):
     """The oracle's output for wl with the physical block ids renumbered
     0, 1, .. in order of first use (aliasing kept): the attention does not
