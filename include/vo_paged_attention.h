@@ -452,6 +452,11 @@ typedef struct vo_bm_stats {
 int32_t vo_bm_create(uint64_t num_blocks, uint64_t block_size, int32_t prefix_caching,
                      vo_block_manager **out);
 void vo_bm_destroy(vo_block_manager *bm);
+/* Test hook, no reference counterpart: with on != 0 a block's hash covers
+ * its own tokens only, so that equal blocks after different prefixes collide
+ * on purpose (the tests of the prefix cache's collision handling).  Only
+ * before the first sequence; VO_ERR_INVALID_ARGUMENT otherwise. */
+int32_t vo_bm_test_unchained_hash(vo_block_manager *bm, int32_t on);
 /* Admits a sequence with its prompt and gives it ceil(n / bs) blocks;
  * *cached_tokens = prompt tokens whose KV the prefix cache already holds
  * (a multiple of bs; the step computes the rest). */

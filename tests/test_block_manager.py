@@ -14,14 +14,13 @@ tokens and of every block's contents, and after each step checks:
   * a prefix-cache hit only ever hands out a block whose whole prefix (its
     tokens and every token before it, which its KV at layers >= 1 depends
     on) equals the prompt's, also when block hashes are made to collide on
-    purpose (VO_BM_TEST_UNCHAINED_HASH: a block hashes its own tokens only);
+    purpose (the vo_bm_test_unchained_hash hook: a block hashes its own tokens
+    only);
   * copy on write only copies a block another live sequence still uses, into
     a block nobody else uses;
   * blocks no live table references are all available again;
   * a request the pool cannot serve raises CapacityError and changes nothing.
 """
-import os
-
 import numpy as np
 import pytest
 from hypothesis import HealthCheck, settings
@@ -39,12 +38,9 @@ class BlockManagerMachine(RuleBasedStateMachine):
     @initialize(num_blocks=st.integers(4, 40), bs=st.sampled_from([1, 2, 4, 16]),
                 caching=st.booleans())
     def setup(self, num_blocks, bs, caching):
+        self.bm = vo.BlockManager(num_blocks, bs, prefix_caching=caching)
         if self.unchained:
-            os.environ["VO_BM_TEST_UNCHAINED_HASH"] = "1"
-        try:
-            self.bm = vo.BlockManager(num_blocks, bs, prefix_caching=caching)
-        finally:
-            os.environ.pop("VO_BM_TEST_UNCHAINED_HASH", None)
+            self.bm.test_unchained_hash(True)
         self.N, self.bs, self.caching = num_blocks, bs, caching
         self.seqs = {}        # seq id -> list of tokens
         # block id -> the tokens up to the end of that full block (model): its
@@ -175,15 +171,14 @@ TestBlockManagerCollidingHashes = CollidingHashMachine.TestCase
 TestBlockManagerCollidingHashes.settings = TestBlockManagerStateMachine.settings
 
 
-def test_prefix_hit_needs_the_same_verified_prefix(monkeypatch):
+def test_prefix_hit_needs_the_same_verified_prefix():
     """A cached block is reused only after the very block the lookup accepted
-    before it.  With VO_BM_TEST_UNCHAINED_HASH=1 a block hashes its own tokens
-    only, so block T after prefix A and block T after prefix B collide: the
-    prompt B + T finds sequence 1's T block (computed after A) and must not
-    take it; A + T still hits both blocks."""
-    monkeypatch.setenv("VO_BM_TEST_UNCHAINED_HASH", "1")
+    before it.  With the unchained-hash test hook a block hashes its own
+    tokens only, so block T after prefix A and block T after prefix B
+    collide: the prompt B + T finds sequence 1's T block (computed after A)
+    and must not take it; A + T still hits both blocks."""
     bm = vo.BlockManager(32, 4)
-    monkeypatch.delenv("VO_BM_TEST_UNCHAINED_HASH")
+    bm.test_unchained_hash(True)
     A, B, T = [1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12]
     assert bm.add_sequence(1, A + T + [0]) == 0
     assert bm.add_sequence(2, B + [0]) == 0
@@ -193,6 +188,45 @@ def test_prefix_hit_needs_the_same_verified_prefix(monkeypatch):
     assert bm.add_sequence(4, T + [0]) == 0          # T was cached at position 1, not 0
     assert bm.add_sequence(5, A + T + [7]) == 8
     assert list(bm.block_table(5)[:2]) == list(bm.block_table(1)[:2])
+    bm.check()
+
+
+def test_duplicate_prompt_then_appends_stay_reachable():
+    """The same prompt twice: the second copy's last-token block duplicates
+    the first's cached block (first writer wins), so the cache's block stands
+    for it in its verified chain.  The blocks it fills afterwards are
+    registered after that block, so a later prompt with the second copy's
+    tokens hits all of them; and a block whose predecessor has no verified
+    link is not registered at all (it could never be hit, and would only hold
+    a hash another sequence's valid block needs)."""
+    bm = vo.BlockManager(64, 4)
+    P = list(range(12))                              # 3 full blocks
+    assert bm.add_sequence(1, P) == 0
+    assert bm.add_sequence(2, P) == 8                # not the last token's block
+    for t in [20, 21, 22, 23]:                       # fills block 3 of sequence 2 only
+        bm.append_token(2, t)
+    assert bm.add_sequence(3, P + [20, 21, 22, 23, 5]) == 16
+    assert list(bm.block_table(3)[:4]) == [bm.block_table(1)[0], bm.block_table(1)[1],
+                                           bm.block_table(1)[2], bm.block_table(2)[3]]
+    for t in [30, 31, 32, 33]:                       # both fill block 3 alike
+        bm.append_token(1, t)
+    assert bm.add_sequence(4, P + [30, 31, 32, 33, 9]) == 16
+    assert bm.block_table(4)[3] == bm.block_table(1)[3]
+    bm.check()
+    # Unchained hashes: sequence 6's block [9, 9, 9, 9] collides with the
+    # cache's entry from sequence 5 (after another prefix), so its chain
+    # breaks there, and its later block is not registered.
+    bm = vo.BlockManager(64, 4)
+    bm.test_unchained_hash(True)
+    assert bm.add_sequence(5, [1, 1, 1, 1, 9, 9, 9, 9, 0]) == 0
+    assert bm.add_sequence(6, [2, 2, 2, 2, 9, 9, 9, 9, 7, 7, 7, 7, 0]) == 0
+    assert bm.add_sequence(7, [3, 3, 3, 3, 7, 7, 7, 7, 0]) == 0   # [7]*4 was not registered
+    assert bm.add_sequence(8, [2, 2, 2, 2, 9, 9, 9, 9, 7, 7, 7, 7, 1]) == 4
+    # so the hash of [7]*4 was free for sequence 7's own block, which a prompt
+    # with sequence 7's prefix now hits
+    assert bm.add_sequence(9, [3, 3, 3, 3, 7, 7, 7, 7, 2]) == 8
+    with pytest.raises(vo.InvalidArgument):
+        bm.test_unchained_hash(False)                # only before the first sequence
     bm.check()
 
 

@@ -45,6 +45,22 @@ def _out(wl, backend):
     return backend.prefill_attention(wl.q, wl.pool, wl.layer, wl.meta)
 
 
+def _out_with_prefill_instances(vo, wl, backend):
+    """_out with per-launch timing on; also the set of prefill kernel
+    instances that ran (the library times each launch under its instance's
+    name: prefill_dma = 64-row workgroups, prefill_dma_narrow = 32-row
+    workgroups, prefill_regs = the register-staged kernel)."""
+    import torch
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    try:
+        out = _out(wl, backend)
+        torch.cuda.synchronize()
+    finally:
+        vo.enable_profiling(False)
+    return out, {k for k in vo.profile() if k.startswith("prefill_")}
+
+
 def _out_replanned(wl, backend):
     """_out after uploading the metadata again, so that the launch plan is
     rebuilt under the current VO_DECODE_* settings (an unchanged meta object
@@ -516,7 +532,8 @@ def test_prefill_64_row_workgroups_edge_shapes(vo, gpu_backend, monkeypatch, off
                  context_lens=[0, 5, 63, 64, 65, 1000, 2047, 31],
                  num_new=[2, 31, 32, 33, 64, 65, 129, 200], seed=61)
     gpu_backend.step_meta(wl.pool).holds = None
-    out = _out(wl, gpu_backend)
+    out, ran = _out_with_prefill_instances(vo, wl, gpu_backend)
+    assert ran == {"prefill_dma"}, ran  # the setting is honoured: 64-row workgroups ran
     want = W.oracle_attention(orc, wl)
     _assert_close(out.float().cpu().numpy(), want, f"prefill 64-row workgroups ({offset})")
 
@@ -548,7 +565,8 @@ def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, f
     wl.ctx_kv[0] = (keys, wl.ctx_kv[0][1])
     wl.host["ctx"][0] = (keys.float().cpu().numpy(), wl.host["ctx"][0][1])
     gpu_backend.step_meta(wl.pool).holds = None
-    out = _out(wl, gpu_backend)
+    out, ran = _out_with_prefill_instances(vo, wl, gpu_backend)
+    assert ran == ({"prefill_dma_narrow"} if narrow == "1" else {"prefill_dma"}), ran
     want = W.oracle_attention(orc, wl)
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()

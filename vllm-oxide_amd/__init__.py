@@ -137,6 +137,7 @@ SIGNATURES = {
                                                       _vp, _vp, _vp, _vp, _vp, _vp]),
     "vo_bm_create": (ctypes.c_int32, [_u64, _u64, ctypes.c_int32, ctypes.POINTER(_vp)]),
     "vo_bm_destroy": (None, [_vp]),
+    "vo_bm_test_unchained_hash": (ctypes.c_int32, [_vp, ctypes.c_int32]),
     "vo_bm_add_sequence": (ctypes.c_int32, [_vp, _u64, _u32p, _u64, _u64p]),
     "vo_bm_append_token": (ctypes.c_int32, [_vp, _u64, ctypes.c_uint32, _u32p, _u32p, _u32p]),
     "vo_bm_fork": (ctypes.c_int32, [_vp, _u64, _u64]),
@@ -722,6 +723,12 @@ class BlockManager:
         self._h = _vp()
         _check(lib.vo_bm_create(num_blocks, block_size, int(prefix_caching), ctypes.byref(self._h)))
         self.num_blocks, self.block_size = num_blocks, block_size
+
+    def test_unchained_hash(self, on: bool = True) -> None:
+        """Test hook: block hashes cover a block's own tokens only, so equal
+        blocks after different prefixes collide on purpose.  Only before the
+        first sequence."""
+        _check(lib.vo_bm_test_unchained_hash(self._h, int(on)))
 
     def add_sequence(self, seq_id: int, tokens) -> int:
         """Admit a sequence with its prompt; returns the prompt tokens already cached."""

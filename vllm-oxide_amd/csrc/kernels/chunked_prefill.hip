@@ -764,13 +764,11 @@ bool prefill_fixed_offset() {
     return !(v && std::string(v) == "running");
 }
 
-// VO_PREFILL_NARROW=0 keeps 64-row workgroups on small grids (A/B).
+// VO_PREFILL_NARROW=0 keeps 64-row workgroups on small grids (A/B).  Read at
+// every launch.
 bool prefill_narrow_enabled() {
-    static const bool on = [] {
-        const char *v = std::getenv("VO_PREFILL_NARROW");
-        return !(v && std::string(v) == "0");
-    }();
-    return on;
+    const char *v = std::getenv("VO_PREFILL_NARROW");
+    return !(v && std::string(v) == "0");
 }
 
 template <int HD, int G, int R>
@@ -780,7 +778,6 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
     constexpr int HALVES = kQT / (kRG * R);
     const uint64_t grid = static_cast<uint64_t>(plan.num_items) * HALVES * pool.kv_heads;
     if (grid > 0x7fffffffull || plan.num_long > plan.num_items) return hipErrorInvalidValue;
-    KernelTimer timer("prefill_mfma", stream);
     // The DMA kernel stages a sequence's whole block table in LDS, and its
     // three 32 KiB stages at head_dim 128 leave room for one workgroup per
     // CU, which takes 8 wavefronts to fill the SIMDs -- or 4 when the grid
@@ -794,7 +791,10 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
             regs_items = plan.num_long;
     }
     const uint32_t per_item = HALVES * pool.kv_heads;
+    // Each launch is timed (when profiling is on) under the name of its
+    // kernel instance, so that a caller can tell which one ran.
     if (regs_items != 0) {
+        KernelTimer timer("prefill_regs", stream);
         hipLaunchKernelGGL((prefill_mfma_kernel<HD, G, R>), dim3(regs_items * per_item),
                            dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
                            meta.table_off, meta.tables, plan.work, q, out, num_heads, scale_log2);
@@ -802,6 +802,7 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
     }
     if constexpr (dma_shape) {
         if (regs_items < plan.num_items) {
+            KernelTimer timer(G == 4 && R == 1 ? "prefill_dma_narrow" : "prefill_dma", stream);
             hipLaunchKernelGGL((prefill_dma_kernel<HD, G, R>),
                                dim3((plan.num_items - regs_items) * per_item), dim3(64 * G * R), 0,
                                stream, pool.k, pool.v, pool.kv_heads, meta.table_off, meta.tables,

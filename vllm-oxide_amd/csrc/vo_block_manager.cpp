@@ -78,6 +78,14 @@ struct Seq {
     std::vector<uint32_t> table;
     std::vector<uint32_t> tokens;
     std::vector<uint64_t> hashes;  // chained hash of each full block
+    // The verified chain: for each full block i, the cached block that
+    // stands for it in the prefix cache -- the sequence's own block once
+    // registered, or an equal block the cache already held for this prefix
+    // -- with that block's generation then; kNone where there is none (the
+    // hash is held by a block that is not this prefix's, or the chain broke
+    // earlier).  A later block is registered with chain[i - 1] as its parent.
+    std::vector<uint32_t> chain;
+    std::vector<uint64_t> chain_gen;
 };
 
 }  // namespace
@@ -85,9 +93,8 @@ struct Seq {
 struct vo_block_manager {
     uint64_t num_blocks = 0, block_size = 0;
     bool prefix_caching = false;
-    // Test hook (VO_BM_TEST_UNCHAINED_HASH=1 at creation): hash a block's
-    // own tokens only, so that equal blocks after different prefixes
-    // collide on purpose.
+    // Test hook (vo_bm_test_unchained_hash): hash a block's own tokens only,
+    // so that equal blocks after different prefixes collide on purpose.
     bool unchained_hash = false;
     std::vector<Block> blocks;
     std::vector<uint32_t> free_list;       // LIFO
@@ -157,31 +164,57 @@ struct vo_block_manager {
         return fnv1a(fnv1a(kFnvOffset, &prev, sizeof(prev)), toks, block_size * sizeof(uint32_t));
     }
 
-    // Whether cached block b may stand at position i of a prompt whose
-    // blocks 0 .. i-1 were accepted as `hits` and whose block i holds toks.
-    bool accepts(uint32_t b, const std::vector<uint32_t> &hits, const uint32_t *toks) const {
+    // Whether cached block b may stand at a position whose predecessor in
+    // the verified chain is `parent` (kNone at position 0, taken at
+    // generation parent_gen) and whose tokens are toks.
+    bool accepts(uint32_t b, uint32_t parent, uint64_t parent_gen, const uint32_t *toks) const {
         const Block &k = blocks[b];
         if (!std::equal(k.tokens.begin(), k.tokens.end(), toks)) return false;
-        if (hits.empty()) return k.parent == kNone;
-        return k.parent == hits.back() && k.parent_gen == blocks[hits.back()].gen;
+        if (parent == kNone) return k.parent == kNone;
+        return k.parent == parent && k.parent_gen == parent_gen && blocks[parent].gen == parent_gen;
     }
 
-    // Registers full block i of `s` in the prefix cache (first writer wins).
+    // Full block i of `s` (blocks 0 .. i-1 done): its chained hash, its link
+    // in the verified chain, and -- when the cache holds nothing under its
+    // hash and its predecessor is verified -- its registration, with that
+    // predecessor as parent.  An equal block already cached for this prefix
+    // stands for it instead; a hash held by a block of another prefix (a
+    // collision, or the cache's first writer for another chain) leaves the
+    // chain broken from here on, so no entry is made that no lookup could
+    // accept.
     void register_full(Seq &s, uint64_t i) {
         const uint64_t prev = i ? s.hashes[i - 1] : 0;
-        const uint64_t h = block_hash(prev, s.tokens.data() + i * block_size);
+        const uint32_t *toks = s.tokens.data() + i * block_size;
+        const uint64_t h = block_hash(prev, toks);
         if (s.hashes.size() <= i) s.hashes.resize(i + 1);
         s.hashes[i] = h;
+        if (s.chain.size() <= i) {
+            s.chain.resize(i + 1, kNone);
+            s.chain_gen.resize(i + 1, 0);
+        }
+        s.chain[i] = kNone;
         if (!prefix_caching) return;
+        const uint32_t parent = i ? s.chain[i - 1] : kNone;
+        const uint64_t parent_gen = i ? s.chain_gen[i - 1] : 0;
+        if (i && (parent == kNone || blocks[parent].gen != parent_gen)) return;
+        auto it = cache.find(h);
+        if (it != cache.end()) {
+            if (accepts(it->second, parent, parent_gen, toks)) {
+                s.chain[i] = it->second;
+                s.chain_gen[i] = blocks[it->second].gen;
+            }
+            return;
+        }
         const uint32_t b = s.table[i];
-        if (blocks[b].hashed || cache.count(h)) return;
+        if (blocks[b].hashed) return;  // registered under another hash
         blocks[b].hashed = true;
         blocks[b].hash = h;
-        blocks[b].parent = i ? s.table[i - 1] : kNone;
-        blocks[b].parent_gen = i ? blocks[s.table[i - 1]].gen : 0;
-        blocks[b].tokens.assign(s.tokens.begin() + i * block_size,
-                                s.tokens.begin() + (i + 1) * block_size);
+        blocks[b].parent = parent;
+        blocks[b].parent_gen = parent_gen;
+        blocks[b].tokens.assign(toks, toks + block_size);
         cache.emplace(h, b);
+        s.chain[i] = b;
+        s.chain_gen[i] = blocks[b].gen;
     }
 };
 
@@ -212,8 +245,6 @@ extern "C" int32_t vo_bm_create(uint64_t num_blocks, uint64_t block_size, int32_
     bm->num_blocks = num_blocks;
     bm->block_size = block_size;
     bm->prefix_caching = prefix_caching != 0;
-    const char *unchained = std::getenv("VO_BM_TEST_UNCHAINED_HASH");
-    bm->unchained_hash = unchained && std::string(unchained) == "1";
     bm->blocks.resize(num_blocks);
     bm->free_list.reserve(num_blocks);
     // Hand out low block ids first.
@@ -227,6 +258,16 @@ extern "C" int32_t vo_bm_create(uint64_t num_blocks, uint64_t block_size, int32_
 }
 
 extern "C" void vo_bm_destroy(vo_block_manager *bm) { delete bm; }
+
+extern "C" int32_t vo_bm_test_unchained_hash(vo_block_manager *bm, int32_t on) {
+    const char *op = "block_manager_test_unchained_hash";
+    if (!bm) return fail_argument(op, "null manager");
+    if (!bm->seqs.empty() || !bm->cache.empty())
+        return fail_argument(op, "only before the first sequence");
+    bm->unchained_hash = on != 0;
+    clear_error();
+    return VO_OK;
+}
 
 extern "C" int32_t vo_bm_add_sequence(vo_block_manager *bm, uint64_t seq_id,
                                       const uint32_t *tokens, uint64_t num_tokens,
@@ -246,7 +287,10 @@ extern "C" int32_t vo_bm_add_sequence(vo_block_manager *bm, uint64_t seq_id,
         for (uint64_t i = 0; (i + 1) * bs < num_tokens; ++i) {
             const uint64_t h = bm->block_hash(prev, tokens + i * bs);
             auto it = bm->cache.find(h);
-            if (it == bm->cache.end() || !bm->accepts(it->second, hits, tokens + i * bs)) break;
+            const uint32_t parent = hits.empty() ? kNone : hits.back();
+            const uint64_t parent_gen = hits.empty() ? 0 : bm->blocks[parent].gen;
+            if (it == bm->cache.end() || !bm->accepts(it->second, parent, parent_gen, tokens + i * bs))
+                break;
             hits.push_back(it->second);
             hit_hashes.push_back(h);
             prev = h;
@@ -265,6 +309,8 @@ extern "C" int32_t vo_bm_add_sequence(vo_block_manager *bm, uint64_t seq_id,
         s.table.push_back(b);
     }
     s.hashes = hit_hashes;
+    s.chain = hits;
+    for (uint32_t b : hits) s.chain_gen.push_back(bm->blocks[b].gen);
     for (uint64_t i = 0; i < fresh; ++i) s.table.push_back(bm->take());
     for (uint64_t i = hits.size(); (i + 1) * bs <= num_tokens; ++i) bm->register_full(s, i);
     bm->stats.hit_blocks += hits.size();
