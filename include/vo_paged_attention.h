@@ -330,6 +330,27 @@ int32_t vo_step_meta_decode_plan(const vo_step_meta *meta, uint64_t *work_items,
 int32_t vo_step_meta_upload_slots(vo_step_meta *meta, const uint32_t *slots, uint64_t num_slots,
                                   void *stream);
 
+/* The trait's form of the two uploads: Backend::prefill_attention and
+ * decode_attention (mod.rs:121-149) take `meta: &PrefillMeta` / `&DecodeMeta`
+ * at every layer, so an implementation of the trait calls these with the
+ * meta's arrays before each attention call.  Same arguments, checks and
+ * errors as vo_step_meta_upload_prefill / _decode; when the meta's last
+ * upload is a step of the same kind whose every array holds the same values
+ * (compared on the host, element by element: the caller may refill the same
+ * buffers for the next step), nothing is uploaded or planned again and the
+ * call returns VO_OK. */
+int32_t vo_step_meta_sync_prefill(vo_step_meta *meta, uint64_t block_size, uint64_t num_seqs,
+                                  const uint64_t *table_off, const uint32_t *tables,
+                                  const uint64_t *context_lens, const uint64_t *seq_row_starts,
+                                  uint64_t num_rows, const uint32_t *positions,
+                                  const uint32_t *slot_mapping, const uint64_t *row_seq,
+                                  const uint64_t *row_num_keys, void *stream);
+int32_t vo_step_meta_sync_decode(vo_step_meta *meta, uint64_t block_size, uint64_t num_seqs,
+                                 const uint64_t *table_off, const uint32_t *tables,
+                                 const uint32_t *positions, const uint32_t *slot_mapping,
+                                 const uint64_t *row_seq, const uint64_t *row_num_keys,
+                                 void *stream);
+
 /* ------------------------------------------------------------------ */
 /* Ops                                                                 */
 /* ------------------------------------------------------------------ */
@@ -345,6 +366,18 @@ int32_t vo_step_meta_upload_slots(vo_step_meta *meta, const uint32_t *slots, uin
  * ordering guarantee on a GPU. */
 int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *keys, const void *values,
                     uint64_t rows, uint64_t cols, const vo_step_meta *meta, void *stream);
+
+/* Backend::write_kv with the trait's own arguments (mod.rs:107-119:
+ * `slots: &[u32]`): the slots [num_slots] are host values.  Checks rows ==
+ * num_slots, cols and layer first (VO_ERR_SHAPE, nothing uploaded).  When
+ * the meta's last upload holds exactly these slots (the model passes the
+ * step's slot mapping, model.rs:289-292) it runs vo_write_kv on them;
+ * otherwise it uploads them as vo_step_meta_upload_slots does (replacing the
+ * meta's last upload; a later vo_step_meta_sync_* uploads the step again)
+ * and then runs vo_write_kv.  Errors: those of vo_write_kv. */
+int32_t vo_write_kv_slots(vo_kv_pool *pool, uint64_t layer, const void *keys, const void *values,
+                          uint64_t rows, uint64_t cols, const uint32_t *slots, uint64_t num_slots,
+                          vo_step_meta *meta, void *stream);
 
 /* write_kv followed by decode_attention on the same decode step
  * (model.rs:310-316: the step's new keys are cached, then attended), in one
@@ -526,6 +559,18 @@ void vo_rope_table_destroy(vo_rope_table *table);
 int32_t vo_rope(const vo_rope_table *table, void *x, uint64_t rows, uint64_t cols,
                 uint64_t head_dim, const vo_step_meta *meta, void *stream);
 
+/* Backend::rope with the trait's own arguments (mod.rs:105: `positions:
+ * &[u32]`): positions [num_positions] are host values.  Checks and errors
+ * as vo_rope, on these positions.  When the meta's last upload holds exactly
+ * these positions the kernel reads the meta's device copy; otherwise they
+ * go to a device array of the meta's own (at most max_rows values,
+ * VO_ERR_CAPACITY), copied from pinned staging on `stream` only when the
+ * values differ from that array's last contents.  The meta's last upload is
+ * left as it is.  Calls on one meta are ordered by `stream`. */
+int32_t vo_rope_positions(const vo_rope_table *table, void *x, uint64_t rows, uint64_t cols,
+                          uint64_t head_dim, const uint32_t *positions, uint64_t num_positions,
+                          vo_step_meta *meta, void *stream);
+
 /* The layer's "rope(q); rope(k); write_kv(k, v)" (model.rs:307-311) as one
  * launch.  No counterpart in the reference's op list: it fuses three of its
  * ops.  queries [rows, q_cols] are rotated in place (as Backend::rope leaves
@@ -574,6 +619,20 @@ int32_t vo_rmsnorm(const float *x, uint64_t rows, uint64_t cols, const void *wei
 int32_t vo_rmsnorm_last_rows(const float *x, uint64_t rows, uint64_t cols, const void *weight,
                              uint64_t weight_len, float eps, const vo_step_meta *meta, void *out,
                              void *stream);
+
+/* Backend::gather_rows (mod.rs:167; cpu/mod.rs:360-368): row i of out
+ * [num_rows_idx, cols] = row row_idx[i] of x [rows, cols], both of `dtype`
+ * (VO_DTYPE_F32 for the residual stream, or VO_DTYPE_BF16); row_idx are host
+ * values.  Check (arena/ops.rs:242-244): the first index >= rows fails with
+ * VO_ERR_SHAPE "gather_rows: row {r} of x [rows, cols]".  Rows must be whole
+ * 4-byte words (a bf16 row of odd width is VO_ERR_ARGUMENT) and out must not
+ * overlap x.  When row_idx are the meta's last rows (PrefillMeta::last_rows,
+ * paged.rs:153-159) the kernel reads the meta's device copy; otherwise a
+ * device array of the meta's own, refilled from pinned staging on `stream`
+ * when the values change (at most max_rows, VO_ERR_CAPACITY). */
+int32_t vo_gather_rows(const void *x, int32_t dtype, uint64_t rows, uint64_t cols,
+                       const uint32_t *row_idx, uint64_t num_rows_idx, vo_step_meta *meta,
+                       void *out, void *stream);
 
 /* Backend::add (mod.rs:161; cpu/mod.rs:351-358): sum [rows, cols] f32 += x
  * [rows, cols] of x_dtype.  The model's residual adds also run fused into

@@ -127,7 +127,14 @@ SIGNATURES = {
     "vo_step_meta_upload_decode": (ctypes.c_int32, [_vp, _u64, _u64, _u64p, _u32p, _u32p,
                                                     _u32p, _u64p, _u64p, _vp]),
     "vo_step_meta_upload_slots": (ctypes.c_int32, [_vp, _u32p, _u64, _vp]),
+    "vo_step_meta_sync_prefill": (ctypes.c_int32, [_vp, _u64, _u64, _u64p, _u32p, _u64p,
+                                                   _u64p, _u64, _u32p, _u32p, _u64p, _u64p,
+                                                   _vp]),
+    "vo_step_meta_sync_decode": (ctypes.c_int32, [_vp, _u64, _u64, _u64p, _u32p, _u32p,
+                                                  _u32p, _u64p, _u64p, _vp]),
     "vo_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _vp, _vp]),
+    "vo_write_kv_slots": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _u32p, _u64, _vp,
+                                           _vp]),
     "vo_prefill_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
     "vo_decode_attention": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _vp]),
     "vo_decode_attention_static": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, _vp, _vp, _u64,
@@ -151,6 +158,7 @@ SIGNATURES = {
                                               ctypes.c_int32, ctypes.POINTER(_vp)]),
     "vo_rope_table_destroy": (None, [_vp]),
     "vo_rope": (ctypes.c_int32, [_vp, _vp, _u64, _u64, _u64, _vp, _vp]),
+    "vo_rope_positions": (ctypes.c_int32, [_vp, _vp, _u64, _u64, _u64, _u32p, _u64, _vp, _vp]),
     "vo_rope_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _vp, _vp, _u64, _u64, _vp,
                                           _vp]),
     "vo_qkv_rope_write_kv": (ctypes.c_int32, [_vp, _u64, _vp, _vp, _u64, _u64, _u64, _vp, _vp,
@@ -165,6 +173,8 @@ SIGNATURES = {
     "vo_rmsnorm": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp, _vp]),
     "vo_rmsnorm_last_rows": (ctypes.c_int32, [_vp, _u64, _u64, _vp, _u64, ctypes.c_float, _vp,
                                               _vp, _vp]),
+    "vo_gather_rows": (ctypes.c_int32, [_vp, ctypes.c_int32, _u64, _u64, _u32p, _u64, _vp, _vp,
+                                        _vp]),
     "vo_add": (ctypes.c_int32, [_vp, _vp, ctypes.c_int32, _u64, _u64, _vp]),
     "vo_silu_mul": (ctypes.c_int32, [_vp, _u64, _vp, _u64, _u64, _u64, _vp, _u64, _vp]),
     "vo_argmax": (ctypes.c_int32, [_vp, ctypes.c_int32, _u64, _u64, _u32p, _u32p, _vp]),
@@ -539,6 +549,29 @@ class StepMeta:
             raise TypeError(f"cannot upload {type(meta).__name__}")
         self.holds = meta
 
+    def sync(self, meta, stream=None) -> None:
+        """vo_step_meta_sync_prefill / _decode: upload ``meta`` unless the last
+        upload holds exactly its values (compared in the library, element by
+        element, so a meta refilled in place is seen)."""
+        off, flat = _csr(meta.block_tables)
+        pos = _u32(meta.positions)
+        slots = _u32(meta.slot_mapping)
+        rseq = _u64a(meta.row_seq)
+        rkeys = _u64a(meta.row_num_keys)
+        if isinstance(meta, PrefillMeta):
+            _check(lib.vo_step_meta_sync_prefill(
+                self._h, meta.block_size, meta.num_seqs(), _p64(off), _p32(flat),
+                _p64(_u64a(meta.context_lens)), _p64(_u64a(meta.seq_row_starts)),
+                meta.num_rows(), _p32(pos), _p32(slots), _p64(rseq), _p64(rkeys),
+                _stream_ptr(stream)))
+        elif isinstance(meta, DecodeMeta):
+            _check(lib.vo_step_meta_sync_decode(
+                self._h, meta.block_size, meta.num_seqs(), _p64(off), _p32(flat), _p32(pos),
+                _p32(slots), _p64(rseq), _p64(rkeys), _stream_ptr(stream)))
+        else:
+            raise TypeError(f"cannot upload {type(meta).__name__}")
+        self.holds = meta
+
     def upload_tokens(self, tokens, stream=None) -> None:
         """The step's token ids (vo_step_meta_upload_tokens)."""
         t = _u32(tokens) if len(tokens) else np.zeros(1, np.uint32)
@@ -902,6 +935,15 @@ class HipBackend:
         _check(lib.vo_rope(table.handle, _dev_ptr(x), x.shape[0], x.shape[1], head_dim, m.handle,
                            _stream_ptr(stream)))
 
+    def rope_positions(self, table: RopeTable, x, pool: KvPool, positions, head_dim: int,
+                       stream=None) -> None:
+        """Backend::rope with the trait's arguments: rotates x [rows, cols] in
+        place at host ``positions`` [rows] (vo_rope_positions)."""
+        m = self.step_meta(pool)
+        p = _u32(positions) if len(positions) else np.zeros(1, np.uint32)
+        _check(lib.vo_rope_positions(table.handle, _dev_ptr(x), x.shape[0], x.shape[1], head_dim,
+                                     _p32(p), len(positions), m.handle, _stream_ptr(stream)))
+
     def rope_write_kv(self, pool: KvPool, layer: int, table: RopeTable, queries, keys, values,
                       meta, stream=None) -> None:
         """rope(q); rope(k); write_kv(k, v) in one launch (q rotated in place)."""
@@ -964,6 +1006,20 @@ class HipBackend:
         _check(lib.vo_rmsnorm_last_rows(_any_ptr(x, torch.float32), x.shape[0], x.shape[1],
                                         _dev_ptr(weight), weight.numel(), eps, m.handle,
                                         _dev_ptr(out), _stream_ptr(stream)))
+        return out
+
+    def gather_rows(self, x, rows, pool: KvPool, out=None, stream=None):
+        """Backend::gather_rows: out[i] = x[rows[i]], x [T, H] f32 or bf16,
+        host ``rows`` (vo_gather_rows)."""
+        import torch
+        m = self.step_meta(pool)
+        if out is None:
+            out = torch.empty((len(rows), x.shape[1]), dtype=x.dtype, device=x.device)
+        dt = VO_DTYPE_BF16 if x.dtype == torch.bfloat16 else VO_DTYPE_F32
+        r = _u32(rows) if len(rows) else np.zeros(1, np.uint32)
+        _check(lib.vo_gather_rows(_any_ptr(x, x.dtype), dt, x.shape[0], x.shape[1], _p32(r),
+                                  len(rows), m.handle, _any_ptr(out, x.dtype),
+                                  _stream_ptr(stream)))
         return out
 
     def add(self, total, x, stream=None) -> None:

@@ -1,6 +1,6 @@
 // layer_ops.hip -- the Llama layer's ops around attention (model.rs:269-356):
-// embedding lookup, RMSNorm (alone or over the step's last rows), residual
-// add, SwiGLU's silu(gate) * up, and greedy argmax.
+// embedding lookup, RMSNorm (alone or over the step's last rows), row gather,
+// residual add, SwiGLU's silu(gate) * up, and greedy argmax.
 //
 // Numerics: the residual stream is f32 (as the reference's workspace);
 // projections' inputs and outputs that feed a GEMM are bf16.  Every op
@@ -12,6 +12,7 @@
 // Roofline: all HBM-bound.  Algorithmic bytes per row:
 //   embed     2*hidden (table row) + 4*hidden (f32 out)
 //   rmsnorm   4*hidden (x) + 2*hidden (out) (+ the weight, cache-resident)
+//   gather    2 * row bytes (read, written)
 //   add       4*cols (sum read) + 4*cols (written) + 2 or 4*cols (x)
 //   silu_mul  2*2*cols (gate, up) + 2*cols (out)
 //   argmax    4*cols (f32 logits) or 2*cols (bf16)
@@ -78,6 +79,25 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint16_t *__restr
         }
     } else {
         for (uint32_t c = threadIdx.x; c < hidden; c += kThreads) dst[c] = bf16_bits_to_f32(src[c]);
+    }
+}
+
+// Backend::gather_rows (cpu/mod.rs:360-368): out row i = x row rows[i], a
+// byte copy of row_words 4-byte words per row.  One workgroup per output
+// row.  V4: 16-byte accesses (row_words % 4 == 0, both bases 16-byte aligned).
+template <bool V4>
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const uint32_t *__restrict__ x,
+                                                               uint32_t row_words,
+                                                               const uint32_t *__restrict__ rows,
+                                                               uint32_t *__restrict__ out) {
+    const uint32_t i = blockIdx.x;
+    const uint32_t *src = x + static_cast<uint64_t>(rows[i]) * row_words;
+    uint32_t *dst = out + static_cast<uint64_t>(i) * row_words;
+    if constexpr (V4) {
+        for (uint32_t c = threadIdx.x * 4; c < row_words; c += kThreads * 4)
+            *reinterpret_cast<u32x4 *>(dst + c) = *reinterpret_cast<const u32x4 *>(src + c);
+    } else {
+        for (uint32_t c = threadIdx.x; c < row_words; c += kThreads) dst[c] = src[c];
     }
 }
 
@@ -376,6 +396,21 @@ hipError_t launch_rmsnorm(const float *x, uint32_t hidden, const uint16_t *weigh
     else
         hipLaunchKernelGGL((rmsnorm_kernel<false>), dim3(rows), dim3(kThreads), 0, stream, x, hidden,
                            weight, eps, rows_idx, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void *x, uint32_t row_words, const uint32_t *rows,
+                              uint32_t num_rows, void *out, bool vec4, hipStream_t stream) {
+    if (num_rows == 0 || row_words == 0) return hipSuccess;
+    KernelTimer timer("gather_rows", stream);
+    const uint32_t *src = static_cast<const uint32_t *>(x);
+    uint32_t *dst = static_cast<uint32_t *>(out);
+    if (vec4)
+        hipLaunchKernelGGL((gather_rows_kernel<true>), dim3(num_rows), dim3(kThreads), 0, stream, src,
+                           row_words, rows, dst);
+    else
+        hipLaunchKernelGGL((gather_rows_kernel<false>), dim3(num_rows), dim3(kThreads), 0, stream,
+                           src, row_words, rows, dst);
     return hipGetLastError();
 }
 

@@ -129,6 +129,9 @@ hipError_t launch_embed(const uint16_t *table, uint32_t hidden, const uint32_t *
 hipError_t launch_rmsnorm(const float *x, uint32_t hidden, const uint16_t *weight, float eps,
                           const uint32_t *rows_idx, uint32_t rows, uint16_t *out,
                           hipStream_t stream);
+// out row i = x row rows[i], rows of row_words 4-byte words (device rows[]).
+hipError_t launch_gather_rows(const void *x, uint32_t row_words, const uint32_t *rows,
+                              uint32_t num_rows, void *out, bool vec4, hipStream_t stream);
 hipError_t launch_add(float *sum, const void *x, bool x_bf16, uint64_t n, hipStream_t stream);
 hipError_t launch_silu_mul(const uint16_t *gate, uint32_t gate_ld, const uint16_t *up,
                            uint32_t up_ld, uint32_t rows, uint32_t cols, uint16_t *out,

@@ -304,6 +304,35 @@ vo_status upload_common(vo_step_meta *m, MetaKind kind, const char *op, uint64_t
     return VO_OK;
 }
 
+// Whether the n values at `given` equal `held` (same count, same values).
+template <class H, class G>
+bool same_array(const std::vector<H> &held, const G *given, uint64_t n) {
+    if (held.size() != n) return false;
+    if (n && !given) return false;
+    for (uint64_t i = 0; i < n; ++i)
+        if (static_cast<uint64_t>(held[i]) != static_cast<uint64_t>(given[i])) return false;
+    return true;
+}
+
+// Whether the meta's last upload is a `kind` step with exactly these inputs
+// (the common part of the prefill and decode uploads).
+bool holds_step(const vo_step_meta *m, MetaKind kind, uint64_t block_size, uint64_t num_seqs,
+                const uint64_t *table_off, const uint32_t *tables, uint64_t num_rows,
+                const uint32_t *positions, const uint32_t *slot_mapping, const uint64_t *row_seq,
+                const uint64_t *row_num_keys) {
+    if (m->kind != kind || m->block_size != block_size || m->num_seqs != num_seqs ||
+        m->num_rows != num_rows || !table_off)
+        return false;
+    if (!same_array(m->table_off, table_off, num_seqs + 1) ||
+        !same_array(m->tables, tables, table_off[num_seqs]) ||
+        !same_array(m->slots, slot_mapping, num_rows) ||
+        !same_array(m->row_seq, row_seq, num_rows) ||
+        !same_array(m->row_num_keys, row_num_keys, num_rows))
+        return false;
+    if (positions) return m->has_positions && same_array(m->positions, positions, num_rows);
+    return m->positions.empty() && m->has_positions == (num_rows == 0);
+}
+
 // Split-K plan.  Every row's keys are cut into splits of L keys (a multiple
 // of 32, default kDefaultSplit).  L does not depend on the rest of the batch,
 // so a row's arithmetic -- which keys each wavefront accumulates, in which
@@ -820,6 +849,11 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
     if (err == hipSuccess)
         err = hipMalloc(reinterpret_cast<void **>(&m->d_tokens), max_rows * sizeof(uint32_t));
     if (err == hipSuccess) err = m->tokens_stage.create(max_rows * sizeof(uint32_t));
+    if (err == hipSuccess)
+        err = hipMalloc(reinterpret_cast<void **>(&m->d_aux_pos), max_rows * sizeof(uint32_t));
+    if (err == hipSuccess)
+        err = hipMalloc(reinterpret_cast<void **>(&m->d_aux_rows), max_rows * sizeof(uint32_t));
+    if (err == hipSuccess) err = m->aux_stage.create(max_rows * sizeof(uint32_t));
     // Default priority, like every stream here.
     if (err == hipSuccess) err = hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&m->fork, hipEventDisableTiming);
@@ -828,6 +862,9 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
         vo_status rc = fail_device(op, err, hipGetErrorString(err));
         if (m->d_tokens) (void)hipFree(m->d_tokens);
         m->tokens_stage.destroy();
+        if (m->d_aux_pos) (void)hipFree(m->d_aux_pos);
+        if (m->d_aux_rows) (void)hipFree(m->d_aux_rows);
+        m->aux_stage.destroy();
         if (m->d_buf) (void)hipFree(m->d_buf);
         m->stage.destroy();
         if (m->d_part_acc) (void)hipFree(m->d_part_acc);
@@ -848,7 +885,10 @@ extern "C" void vo_step_meta_destroy(vo_step_meta *m) {
     DeviceGuard guard(m->device);
     m->stage.destroy();
     m->tokens_stage.destroy();
+    m->aux_stage.destroy();
     (void)hipFree(m->d_tokens);
+    (void)hipFree(m->d_aux_pos);
+    (void)hipFree(m->d_aux_rows);
     (void)hipFree(m->d_buf);
     (void)hipFree(m->d_part_acc);
     (void)hipFree(m->d_part_ml);
@@ -885,6 +925,8 @@ extern "C" int32_t vo_step_meta_upload_prefill(
         m->kind = kNone;
         return rc;
     }
+    m->context_lens.assign(context_lens, context_lens + num_seqs);
+    m->seq_row_starts.assign(seq_row_starts, seq_row_starts + num_seqs + 1);
     {
         // PrefillMeta::last_rows (paged.rs:153-159).
         const uint32_t *dp;
@@ -964,6 +1006,67 @@ extern "C" int32_t vo_step_meta_upload_slots(vo_step_meta *m, const uint32_t *sl
     if (vo_status rc = finish_upload(m, pk, static_cast<hipStream_t>(stream), op)) return rc;
     clear_error();
     return VO_OK;
+}
+
+namespace vo {
+
+vo_status aux_upload(vo_step_meta *m, std::vector<uint32_t> &held, bool &valid, uint32_t *dev,
+                     const uint32_t *values, uint64_t n, hipStream_t stream, const char *op) {
+    if (valid && same_array(held, values, n)) return VO_OK;
+    if (n > m->max_rows) return fail_capacity("rows per step", n, m->max_rows);
+    if (n == 0) {
+        held.clear();
+        valid = true;
+        return VO_OK;
+    }
+    uint8_t *host;
+    hipError_t err = m->aux_stage.acquire(&host);
+    if (err == hipSuccess) {
+        std::memcpy(host, values, n * sizeof(uint32_t));
+        err = m->aux_stage.commit(dev, n * sizeof(uint32_t), stream);
+    }
+    if (err != hipSuccess) {
+        valid = false;
+        return fail_device(op, err, hipGetErrorString(err));
+    }
+    held.assign(values, values + n);
+    valid = true;
+    return VO_OK;
+}
+
+}  // namespace vo
+
+extern "C" int32_t vo_step_meta_sync_prefill(
+    vo_step_meta *m, uint64_t block_size, uint64_t num_seqs, const uint64_t *table_off,
+    const uint32_t *tables, const uint64_t *context_lens, const uint64_t *seq_row_starts,
+    uint64_t num_rows, const uint32_t *positions, const uint32_t *slot_mapping,
+    const uint64_t *row_seq, const uint64_t *row_num_keys, void *stream) {
+    if (!m) return fail_argument("prefill", "null meta");
+    if (holds_step(m, kPrefill, block_size, num_seqs, table_off, tables, num_rows, positions,
+                   slot_mapping, row_seq, row_num_keys) &&
+        same_array(m->context_lens, context_lens, num_seqs) &&
+        same_array(m->seq_row_starts, seq_row_starts, num_seqs + 1)) {
+        clear_error();
+        return VO_OK;
+    }
+    return vo_step_meta_upload_prefill(m, block_size, num_seqs, table_off, tables, context_lens,
+                                       seq_row_starts, num_rows, positions, slot_mapping, row_seq,
+                                       row_num_keys, stream);
+}
+
+extern "C" int32_t vo_step_meta_sync_decode(vo_step_meta *m, uint64_t block_size,
+                                            uint64_t num_seqs, const uint64_t *table_off,
+                                            const uint32_t *tables, const uint32_t *positions,
+                                            const uint32_t *slot_mapping, const uint64_t *row_seq,
+                                            const uint64_t *row_num_keys, void *stream) {
+    if (!m) return fail_argument("decode", "null meta");
+    if (holds_step(m, kDecode, block_size, num_seqs, table_off, tables, num_seqs, positions,
+                   slot_mapping, row_seq, row_num_keys)) {
+        clear_error();
+        return VO_OK;
+    }
+    return vo_step_meta_upload_decode(m, block_size, num_seqs, table_off, tables, positions,
+                                      slot_mapping, row_seq, row_num_keys, stream);
 }
 
 extern "C" int32_t vo_step_meta_fix_launch(vo_step_meta *m, uint64_t work_headroom,
@@ -1148,6 +1251,29 @@ extern "C" int32_t vo_write_kv(vo_kv_pool *pool, uint64_t layer, const void *key
     return device_status(op, err);
 }
 
+extern "C" int32_t vo_write_kv_slots(vo_kv_pool *pool, uint64_t layer, const void *keys,
+                                     const void *values, uint64_t rows, uint64_t cols,
+                                     const uint32_t *slots, uint64_t num_slots, vo_step_meta *m,
+                                     void *stream) {
+    const char *op = "write_kv";
+    if (!pool || !m) return fail_argument(op, "null pool or meta");
+    if (num_slots && !slots) return fail_argument(op, "null slots");
+    const vo_kv_layout &L = pool->layout;
+    // arena/ops.rs:116-127, before anything is uploaded.
+    if (rows != num_slots || cols != L.kv_heads * L.head_dim || layer >= L.num_layers)
+        return fail_shape(op, "keys [" + std::to_string(rows) + ", " + std::to_string(cols) +
+                                  "], values [" + std::to_string(rows) + ", " +
+                                  std::to_string(cols) + "], " + std::to_string(num_slots) +
+                                  " slots, layer " + std::to_string(layer) + ", pool " +
+                                  layout_text(L));
+    // The step's own slot mapping (the model passes meta.slot_mapping,
+    // model.rs:289-292) is written through the step's plan; other slots
+    // are uploaded first, replacing the meta's last upload.
+    if (m->kind == kNone || !same_array(m->slots, slots, num_slots))
+        if (int32_t rc = vo_step_meta_upload_slots(m, slots, num_slots, stream)) return rc;
+    return vo_write_kv(pool, layer, keys, values, rows, cols, m, stream);
+}
+
 // ---------------------------------------------------------------------------
 // RoPE
 // ---------------------------------------------------------------------------
@@ -1197,24 +1323,27 @@ void rope_host_table(const vo_rope_config &c, uint64_t max_len, std::vector<floa
     }
 }
 
-// cpu/mod.rs:232-247 and arena/ops.rs:86-96 for one operand of rope.
+// cpu/mod.rs:232-247 and arena/ops.rs:86-96 for one operand of rope, whose
+// positions are num_positions host values with maximum max_position (has:
+// whether there are positions at all).
 vo_status check_rope(const char *op, const vo_rope_table *t, uint64_t rows, uint64_t cols,
-                     uint64_t head_dim, const vo_step_meta *m) {
-    const bool shape_ok = m->has_positions && rows == m->num_rows && head_dim > 0 &&
-                          head_dim % 2 == 0 && cols % head_dim == 0;
+                     uint64_t head_dim, bool has, uint64_t num_positions,
+                     const uint32_t *positions, uint32_t max_position) {
+    const bool shape_ok = has && rows == num_positions && head_dim > 0 && head_dim % 2 == 0 &&
+                          cols % head_dim == 0;
     if (!shape_ok)
         return fail_shape(op, "x [" + std::to_string(rows) + ", " + std::to_string(cols) + "], " +
-                                  (m->has_positions ? std::to_string(m->num_rows) : std::string("no")) +
+                                  (has ? std::to_string(num_positions) : std::string("no")) +
                                   " positions, head_dim " + std::to_string(head_dim));
     if (head_dim != 2 * t->half)
         return fail_shape(op, "head_dim " + std::to_string(head_dim) + ", table built for " +
                                   std::to_string(2 * t->half));
-    if (rows && m->max_position >= t->max_len) {
+    if (rows && max_position >= t->max_len) {
         // The first position past the table, in row order (cpu/mod.rs:241).
-        uint64_t pos = m->max_position;
-        for (uint32_t p : m->positions) {
-            if (p >= t->max_len) {
-                pos = p;
+        uint64_t pos = max_position;
+        for (uint64_t r = 0; r < num_positions; ++r) {
+            if (positions[r] >= t->max_len) {
+                pos = positions[r];
                 break;
             }
         }
@@ -1228,6 +1357,29 @@ vo_status check_rope(const char *op, const vo_rope_table *t, uint64_t rows, uint
         return fail(e);
     }
     return VO_OK;
+}
+
+// The device positions for rope over `positions` [rows]: the meta's own when
+// its last upload holds exactly these, else its aux copy.
+vo_status device_positions(vo_step_meta *m, const uint32_t *positions, uint64_t rows,
+                           hipStream_t stream, const char *op, const uint32_t **out) {
+    if (m->kind != kNone && m->has_positions && m->view.positions &&
+        same_array(m->positions, positions, rows)) {
+        *out = m->view.positions;
+        return VO_OK;
+    }
+    if (vo_status rc = aux_upload(m, m->aux_pos, m->aux_pos_valid, m->d_aux_pos, positions, rows,
+                                  stream, op))
+        return rc;
+    *out = m->d_aux_pos;
+    return VO_OK;
+}
+
+// check_rope on the positions of the meta's last upload.
+vo_status check_rope(const char *op, const vo_rope_table *t, uint64_t rows, uint64_t cols,
+                     uint64_t head_dim, const vo_step_meta *m) {
+    return check_rope(op, t, rows, cols, head_dim, m->has_positions, m->num_rows,
+                      m->positions.data(), m->max_position);
 }
 
 }  // namespace
@@ -1291,6 +1443,36 @@ extern "C" int32_t vo_rope(const vo_rope_table *t, void *x, uint64_t rows, uint6
     const hipError_t err = kernels::launch_rope_rows(
         static_cast<uint16_t *>(x), static_cast<uint32_t>(rows), static_cast<uint32_t>(cols),
         static_cast<uint32_t>(t->half), m->view.positions, t->d_cos, t->d_sin,
+        static_cast<hipStream_t>(stream));
+    return device_status(op, err);
+}
+
+extern "C" int32_t vo_rope_positions(const vo_rope_table *t, void *x, uint64_t rows,
+                                     uint64_t cols, uint64_t head_dim, const uint32_t *positions,
+                                     uint64_t num_positions, vo_step_meta *m, void *stream) {
+    const char *op = "rope";
+    if (!t || !m) return fail_argument(op, "null table or meta");
+    if (num_positions && !positions) return fail_argument(op, "null positions");
+    uint32_t max_position = 0;
+    for (uint64_t r = 0; r < num_positions; ++r) max_position = std::max(max_position, positions[r]);
+    if (vo_status rc = check_rope(op, t, rows, cols, head_dim, true, num_positions, positions,
+                                  max_position))
+        return rc;
+    if (rows == 0 || cols == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!x) return fail_argument(op, "null x");
+    if (rows > kU32Limit || cols > kU32Limit) return fail_capacity("rope rows/cols (u32)", std::max(rows, cols), kU32Limit);
+    if (t->half % 8 == 0 && !aligned16(x)) return fail_argument(op, "x must be 16-byte aligned");
+    DeviceGuard guard(t->device);
+    const uint32_t *d_positions = nullptr;
+    if (vo_status rc = device_positions(m, positions, rows, static_cast<hipStream_t>(stream),
+                                        op, &d_positions))
+        return rc;
+    const hipError_t err = kernels::launch_rope_rows(
+        static_cast<uint16_t *>(x), static_cast<uint32_t>(rows), static_cast<uint32_t>(cols),
+        static_cast<uint32_t>(t->half), d_positions, t->d_cos, t->d_sin,
         static_cast<hipStream_t>(stream));
     return device_status(op, err);
 }

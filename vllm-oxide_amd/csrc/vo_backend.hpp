@@ -259,7 +259,35 @@ struct vo_step_meta {
     uint32_t *d_tokens = nullptr;   // [max_rows]
     vo::Staging tokens_stage;       // 2 x [max_rows], pinned
     bool has_tokens = false;
+
+    // A prefill upload's per-sequence inputs, kept to compare a later
+    // vo_step_meta_sync_prefill with.
+    std::vector<uint64_t> context_lens;    // [S]
+    std::vector<uint64_t> seq_row_starts;  // [S+1]
+
+    // Arrays the trait-shaped ops bring with each call (vo_rope_positions'
+    // positions, vo_gather_rows' rows) when they are not the current
+    // upload's: device copies of their own, refilled only when the content
+    // changes (compared with the host copies), through pinned staging.
+    std::vector<uint32_t> aux_pos;       // host copy of d_aux_pos
+    bool aux_pos_valid = false;
+    uint32_t *d_aux_pos = nullptr;       // [max_rows]
+    std::vector<uint32_t> aux_rows;      // host copy of d_aux_rows
+    bool aux_rows_valid = false;
+    uint32_t *d_aux_rows = nullptr;      // [max_rows]
+    vo::Staging aux_stage;               // 2 x [max_rows] u32, pinned
 };
+
+namespace vo {
+
+// A device copy of the n host values `values` in `dev` (one of the meta's
+// aux arrays, of max_rows entries), whose host copy is `held`: refilled by
+// one async copy from the meta's pinned staging on `stream` when the content
+// differs, else left as it is.  VO_ERR_CAPACITY past max_rows.
+vo_status aux_upload(vo_step_meta *m, std::vector<uint32_t> &held, bool &valid, uint32_t *dev,
+                     const uint32_t *values, uint64_t n, hipStream_t stream, const char *op);
+
+}  // namespace vo
 
 struct vo_rope_table {
     int device = 0;

@@ -1,6 +1,6 @@
 // vo_layer.cpp -- the C ABI of the Llama layer's ops around attention:
-// token upload, embed, rmsnorm (alone and over the LM head's rows), add,
-// silu_mul and argmax.  Checks mirror crates/engine/src/arena/ops.rs and
+// token upload, embed, rmsnorm (alone and over the LM head's rows),
+// gather_rows, add, silu_mul and argmax.  Checks mirror crates/engine/src/arena/ops.rs and
 // backend/cpu/mod.rs; kernels are in kernels/layer_ops.hip.
 #include <algorithm>
 #include <cstring>
@@ -134,6 +134,65 @@ extern "C" int32_t vo_rmsnorm_last_rows(const float *x, uint64_t rows, uint64_t 
                                                      static_cast<uint32_t>(m->num_seqs),
                                                      static_cast<uint16_t *>(out),
                                                      static_cast<hipStream_t>(stream)));
+}
+
+namespace {
+
+// Whether rows [n] are the meta's last rows (PrefillMeta::last_rows,
+// paged.rs:153-159; in a decode step every row), so that the meta's device
+// copy serves vo_gather_rows.
+bool are_last_rows(const vo_step_meta *m, const uint32_t *rows, uint64_t n) {
+    if ((m->kind != kPrefill && m->kind != kDecode) || !m->last_rows_ok || !m->d_last_rows ||
+        n != m->num_seqs)
+        return false;
+    for (uint64_t s = 0; s < n; ++s) {
+        const uint64_t last = m->kind == kDecode ? s : m->seq_row_starts[s + 1] - 1;
+        if (rows[s] != last) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" int32_t vo_gather_rows(const void *x, int32_t dtype, uint64_t rows, uint64_t cols,
+                                  const uint32_t *idx, uint64_t num_idx, vo_step_meta *m,
+                                  void *out, void *stream) {
+    const char *op = "gather_rows";
+    if (!m) return fail_argument(op, "null meta");
+    if (dtype != VO_DTYPE_BF16 && dtype != VO_DTYPE_F32)
+        return fail_argument(op, "dtype must be VO_DTYPE_BF16 or VO_DTYPE_F32");
+    if (num_idx && !idx) return fail_argument(op, "null rows");
+    // arena/ops.rs:242-244: the first row past x.
+    for (uint64_t i = 0; i < num_idx; ++i)
+        if (idx[i] >= rows)
+            return fail_shape(op, "row " + std::to_string(idx[i]) + " of x " + shape2(rows, cols));
+    const uint64_t esize = dtype == VO_DTYPE_BF16 ? 2 : 4;
+    const uint64_t row_bytes = cols * esize;
+    if (num_idx == 0 || row_bytes == 0) {
+        clear_error();
+        return VO_OK;
+    }
+    if (!x || !out) return fail_argument(op, "null x or out");
+    if (overlaps(x, rows * row_bytes, out, num_idx * row_bytes))
+        return fail_shape(op, "out overlaps x");
+    if (num_idx > kU32Limit) return fail_capacity("gather_rows rows (u32)", num_idx, kU32Limit);
+    // The kernel copies 4-byte words; a bf16 row of odd width is not whole words.
+    if (row_bytes % 4 != 0 || row_bytes / 4 > kU32Limit || (reinterpret_cast<uintptr_t>(x) & 3) ||
+        (reinterpret_cast<uintptr_t>(out) & 3))
+        return fail_argument(op, "rows must be whole, 4-byte aligned 4-byte words");
+    DeviceGuard guard(m->device);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const uint32_t *d_rows = m->d_last_rows;
+    if (!are_last_rows(m, idx, num_idx)) {
+        if (vo_status rc = aux_upload(m, m->aux_rows, m->aux_rows_valid, m->d_aux_rows, idx,
+                                      num_idx, st, op))
+            return rc;
+        d_rows = m->d_aux_rows;
+    }
+    const bool vec4 = row_bytes % 16 == 0 && aligned16(x) && aligned16(out);
+    return device_status(op, kernels::launch_gather_rows(
+                                 x, static_cast<uint32_t>(row_bytes / 4), d_rows,
+                                 static_cast<uint32_t>(num_idx), out, vec4, st));
 }
 
 extern "C" int32_t vo_add(float *sum, const void *x, int32_t x_dtype, uint64_t rows, uint64_t cols,
