@@ -10,9 +10,18 @@
  *
  *   Backend::alloc_kv_pool   (mod.rs:73-74)   -> vo_kv_pool_create
  *   Backend::kv_layout       (mod.rs:75)      -> vo_kv_pool_layout
- *   Backend::write_kv        (mod.rs:107-119) -> vo_write_kv
- *   Backend::prefill_attention (mod.rs:121-135) -> vo_prefill_attention
- *   Backend::decode_attention  (mod.rs:137-149) -> vo_decode_attention
+ *   Backend::rope            (mod.rs:105)     -> vo_rope_positions (host positions);
+ *                                                  vo_rope (the step upload's)
+ *   Backend::write_kv        (mod.rs:107-119) -> vo_write_kv_slots (host slots);
+ *                                                  vo_write_kv (the step upload's)
+ *   Backend::prefill_attention (mod.rs:121-135) -> vo_step_meta_sync_prefill +
+ *                                                  vo_prefill_attention
+ *   Backend::decode_attention  (mod.rs:137-149) -> vo_step_meta_sync_decode +
+ *                                                  vo_decode_attention
+ *   Backend::gather_rows     (mod.rs:167)     -> vo_gather_rows
+ *   Backend::embed, rmsnorm, matmul, silu_mul, add, argmax (mod.rs:84-175)
+ *                                             -> vo_embed, vo_rmsnorm, vo_matmul,
+ *                                                  vo_silu_mul, vo_add, vo_argmax
  *   Backend::read            (mod.rs:177-181) -> vo_workspace_read; vo_gather_kv
  *                                                  reads the pool (both debug/test only)
  *   Backend::alloc_workspace (mod.rs:76-77)   -> vo_workspace_create

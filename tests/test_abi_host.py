@@ -36,6 +36,20 @@ def test_library_exports_every_declared_symbol(vo):
     assert set(declared) == set(vo.SIGNATURES)
 
 
+def test_integration_extern_block_binds_every_declared_function():
+    """The Rust FFI block of the integration guide (section 2) has one
+    `pub fn` per function the header declares, and no other."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    start = text.index("## 2.")
+    block = text[start:text.index("## 3.", start)]
+    bound = set(re.findall(r"pub fn (vo_[a-z0-9_]+)\(", block))
+    assert bound == set(_declared_functions())
+    statuses = set(re.findall(r"pub const (VO_(?:OK|ERR_[A-Z_]+)): i32", block))
+    header = (ROOT / "include" / "vo_paged_attention.h").read_text()
+    enum = header[header.index("typedef enum vo_status"):header.index("} vo_status;")]
+    assert statuses == set(re.findall(r"\b(VO_(?:OK|ERR_[A-Z_]+)) =", enum))
+
+
 def test_version_and_status_names(vo):
     assert b"gfx950" in vo.lib.vo_version()
     assert vo.lib.vo_status_name(vo.VO_ERR_BLOCK_OUT_OF_RANGE) == b"VO_ERR_BLOCK_OUT_OF_RANGE"

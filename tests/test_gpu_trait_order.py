@@ -76,7 +76,10 @@ def _p64(a):
 
 
 class TraitModel(AbiModel):
-    """AbiModel's forward with each op taking the trait's own host arrays."""
+    """AbiModel's forward with each op taking the trait's own host arrays,
+    and the element types of a backend that sees only the trait's calls:
+    every GEMM output is bf16 except the tied LM head's f32 logits, and add
+    widens bf16 into the f32 residual."""
 
     def _sync(self, h, prefill):
         lib = self.lib
@@ -125,10 +128,10 @@ class TraitModel(AbiModel):
                     chk(self._sync(h, prefill))
                     fn = lib.vo_prefill_attention if prefill else lib.vo_decode_attention
                     chk(fn(P(q), T, qd, self.pool, li, self.meta, P(attn), None))
-                    attn_out = A.alloc(T, H)                              # f32
+                    attn_out = A.alloc(T, H)                              # bf16
                     chk(lib.vo_matmul(self.gemm, P(attn), T, qd, L["wo"].ptr, H, qd,
-                                      P(attn_out), f32, 0, None))
-                    chk(lib.vo_add(P(residual), P(attn_out), f32, T, H, None))
+                                      P(attn_out), bf, 0, None))
+                    chk(lib.vo_add(P(residual), P(attn_out), bf, T, H, None))
                 with A.scope():
                     normed = A.alloc(T, H)
                     chk(lib.vo_rmsnorm(P(residual), T, H, L["mlp_norm"].ptr, H, eps,
@@ -139,10 +142,10 @@ class TraitModel(AbiModel):
                     chk(lib.vo_matmul(self.gemm, P(normed), T, H, L["w_up"].ptr, F, H, P(up),
                                       bf, 0, None))
                     chk(lib.vo_silu_mul(P(gate), F, P(up), F, T, F, P(gate), F, None))
-                    down = A.alloc(T, H)                                  # f32
+                    down = A.alloc(T, H)                                  # bf16
                     chk(lib.vo_matmul(self.gemm, P(gate), T, F, L["w_down"].ptr, H, F, P(down),
-                                      f32, 0, None))
-                    chk(lib.vo_add(P(residual), P(down), f32, T, H, None))
+                                      bf, 0, None))
+                    chk(lib.vo_add(P(residual), P(down), bf, T, H, None))
             normed = A.alloc(S, H)
             if prefill:
                 # gather_rows(residual, meta.last_rows()); rmsnorm   model.rs:337-340
