@@ -459,6 +459,51 @@ def test_decode_cfg5_prefix_shared_full_size(vo, gpu_backend):
     _assert_close(out.float().cpu().numpy(), want, "cfg5")
 
 
+@pytest.mark.parametrize("name", ["cfg2", "cfg5"])
+def test_decode_attention_write_kv_full_size(vo, name):
+    """The call the decode benchmark times, vo_decode_attention_write_kv, at
+    BASELINE config 2 and config 5's full sizes: one launch, bitwise equal to
+    write_kv then decode_attention (the output, and every key and value each
+    sequence reads back from the pool), and within rtol/atol of the oracle.
+    Layer 0 runs the two ops, layer 1 the fused call, on the same cached
+    context; both layers' new slots hold other values first."""
+    import torch
+    _say(f"decode+write_kv full size {name}")
+    if name == "cfg2":
+        ctx, heads, blocks, seed, shared = W.cfg2_context_lens(), 32, 20000, 2, 0
+    else:
+        ctx, heads, blocks, seed, shared = W.cfg5_context_lens(), 64, 40000, 5, 4096
+    backend = vo.HipBackend(device=0, max_seqs=len(ctx), max_rows=W.FILL_ROWS,
+                            max_table_entries=blocks, max_query_heads=heads)
+    wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=blocks, context_lens=ctx, seed=seed,
+                 shared_prefix=shared, shared_count=64 if shared else 0, num_layers=2,
+                 fill_layers=[0, 1])
+    gen = torch.Generator(device="cuda:0").manual_seed(13)
+    junk_k = torch.randn(wl.k_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
+    junk_v = torch.randn(wl.v_new.shape, generator=gen, device="cuda:0").to(torch.bfloat16)
+    for layer in (0, 1):
+        backend.write_kv(wl.pool, layer, junk_k, junk_v, wl.meta)
+    backend.write_kv(wl.pool, 0, wl.k_new, wl.v_new, wl.meta)
+    want = backend.decode_attention(wl.q, wl.pool, 0, wl.meta)
+    vo.profile_reset()
+    vo.enable_profiling(True)
+    got = backend.decode_attention_write_kv(wl.q, wl.k_new, wl.v_new, wl.pool, 1, wl.meta)
+    torch.cuda.synchronize()
+    vo.enable_profiling(False)
+    kernels = set(vo.profile())
+    assert "reshape_and_cache" not in kernels and "decode_splitk" in kernels, kernels
+    assert np.array_equal(_bits(got), _bits(want)), name
+    for s_, c in enumerate(ctx):
+        k0, v0 = backend.read_kv(wl.pool, 0, wl.meta, s_, c + 1)
+        k1, v1 = backend.read_kv(wl.pool, 1, wl.meta, s_, c + 1)
+        assert np.array_equal(_bits(k1), _bits(k0)), f"{name}: K of seq {s_}"
+        assert np.array_equal(_bits(v1), _bits(v0)), f"{name}: V of seq {s_}"
+        assert np.array_equal(_bits(k1[c]), _bits(wl.k_new[s_])), f"{name}: new K of seq {s_}"
+    oracle_want = W.oracle_attention(orc, wl)
+    _assert_close(got.float().cpu().numpy(), oracle_want, name)
+
+
 def test_decode_batch_invariance_bitwise(vo, gpu_backend):
     """A row's output is identical alone or in a batch (the reference's
     batch-invariance invariant, CLAUDE.md; model.rs:539-584)."""

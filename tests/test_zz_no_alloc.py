@@ -76,6 +76,39 @@ def test_static_decode_equals_decode_attention_two_calls(vo, heads):
         assert np.array_equal(_bits(again), _bits(want)), name + " (repeated)"
 
 
+@pytest.mark.parametrize("case", ["3000 short rows", "shared prefix"])
+def test_static_decode_many_rows_and_shared_prefix(vo, case):
+    """Two more shapes, each bitwise equal to vo_decode_attention: 3000
+    short rows (more rows than the plan kernel's 1024 threads, so each thread
+    plans several), and 24 rows aliasing a 2048-key prefix, where
+    vo_decode_attention runs the shared-pack kernel and the static call the
+    register path.  The second call is the smaller one."""
+    import torch
+    rng = np.random.default_rng(17)
+    if case == "3000 short rows":
+        heads, ctx, shared = 16, rng.integers(0, 300, 3000), 0
+        nblocks = int(sum(-(-(int(c) + 1) // 16) for c in ctx)) + 16
+    else:
+        heads, ctx, shared = 32, 2048 + rng.integers(1, 600, 24), 2048
+        nblocks = 4000
+    _say(f"static decode: {case}")
+    backend = vo.HipBackend(device=0, max_seqs=len(ctx), max_rows=W.FILL_ROWS,
+                            max_table_entries=nblocks, max_query_heads=heads)
+    wl = W.build(vo, backend, kind="decode", heads=heads, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=nblocks, context_lens=ctx, seed=19,
+                 shared_prefix=shared, shared_count=len(ctx) if shared else 0, keep_host=False)
+    want = backend.decode_attention(wl.q, wl.pool, 0, wl.meta)
+    work, parts, _ = backend.step_meta(wl.pool).decode_plan()
+    assert (work < parts) == bool(shared), (work, parts)   # packed items over the prefix
+    dmeta, entries = _device_meta(wl)
+    errors = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    rc, got = _static(vo, wl, wl.q, dmeta, entries, int(max(ctx)) + 1, errors)
+    vo._check(rc)
+    torch.cuda.synchronize()
+    assert int(errors.item()) == 0
+    assert np.array_equal(_bits(got), _bits(want)), case
+
+
 def test_static_decode_device_checks_and_capacity(vo):
     import torch
     backend = vo.HipBackend(device=0, max_seqs=8, max_rows=W.FILL_ROWS, max_table_entries=512,
