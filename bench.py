@@ -14,16 +14,20 @@ One step = what the engine does per layer for this batch
 
 value = algorithmic decode bytes per step / step time, in GB/s, where the
 algorithmic bytes are every key's K and V once per KV head (bf16), the q and
-out rows, and the block-table entries.  tokens_per_s = 64 / step time.
+out rows, and the block-table entries.  attention_rows_per_s = 64 / step
+time: one layer's decode attention rows per second (not model tokens).
 roofline.achieved = the same bytes / the split-K kernel's average duration,
 timed live with HIP events around each launch.
 
-The default run prints that cfg2 line with two nested records for the
+The default run prints that cfg2 line with three nested records for the
 north_star's other targets, each with its own roofline and CPU baseline:
 "cfg5" (prefix-shared decode at the Llama-3-70B layer shape, HBM roofline on
-the unique bytes) and "cfg3" (chunked prefill, bf16 MFMA roofline on the
-causal-aware FLOPs).  --config cfg3 / cfg5 / cfg4 / cfg4a print one config's
-full line instead; --headline-only drops the nested records.
+the unique bytes), "cfg3" (chunked prefill, bf16 MFMA roofline on the
+causal-aware FLOPs) and "cfg4" (the full 32-layer mixed step of the
+Llama-3-8B-shaped model: model tokens/s and decode tokens/s, the metric's
+"tokens/s", with the GEMMs' MFMA roofline and per-kernel ms per step).
+--config cfg3 / cfg5 / cfg4 / cfg4a print one config's full line instead;
+--headline-only drops the nested records.
 """
 import argparse
 import ctypes
@@ -224,7 +228,9 @@ def bench_decode(vo, W, orc, args, cfg):
             "layers_rotated": layers,
             "split_keys": int(os.environ.get("VO_DECODE_SPLIT", "2048")),  # the backend's default
         },
-        "tokens_per_s": round(S / sec, 1),
+        # One layer's decode attention: S rows per step (model tokens/s are
+        # the cfg4 record's).
+        "attention_rows_per_s": round(S / sec, 1),
         # HBM bytes move once per physical block, so the fraction of peak is
         # taken on the unique bytes (equal to the algorithmic bytes when no
         # block is shared, as in cfg2).
@@ -273,7 +279,7 @@ def cpu_baseline(orc, W, wl, nbytes, args):
     return {
         "value": round(nbytes / med / 1e9, 2),
         "unit": "GB/s",
-        "tokens_per_s": round(S / med, 2),
+        "attention_rows_per_s": round(S / med, 2),
         "ms_per_step": round(med * 1e3, 2),
         "single_thread_ms_per_step": round(single * 1e3, 2),
         "cores": threads,
@@ -702,9 +708,10 @@ def bench_rope_write(vo, W, orc, args):
 
 def nested_record(line):
     """The fields of a config's own line that the headline line nests."""
-    keep = ("metric", "value", "unit", "ms_per_step", "pct_of_hbm_peak", "tokens_per_s",
-            "kernels_us", "roofline", "cpu_baseline", "algorithmic_bytes_per_step",
-            "unique_bytes_per_step", "steps", "warmup", "settle")
+    keep = ("metric", "value", "unit", "ms_per_step", "pct_of_hbm_peak", "attention_rows_per_s",
+            "decode_tokens_per_s", "kernels_us", "kernels_ms_per_step", "roofline",
+            "cpu_baseline", "algorithmic_bytes_per_step", "unique_bytes_per_step",
+            "gemm_tflop_per_step", "steps", "warmup", "settle")
     out = {k: line[k] for k in keep if k in line}
     out["workload"] = line["config"]["workload"]
     return out
@@ -773,11 +780,14 @@ def main():
                 metric="prefix-shared decode attn GB/s (logical bytes), Llama-3-70B layer")
     lines = []
     if args.config == "cfg2" and not args.headline_only:
-        # The headline (cfg2) line, with the other two north_star targets
-        # nested: cfg5's prefix-shared decode and cfg3's chunked prefill.
+        # The headline (cfg2) line, with the other north_star targets nested:
+        # cfg5's prefix-shared decode, cfg3's chunked prefill and cfg4's full
+        # model step (the metric's tokens/s).
         line = bench_decode(vo, W, orc, args, cfg2)
         line["cfg5"] = nested_record(bench_decode(vo, W, orc, args, cfg5))
         line["cfg3"] = nested_record(bench_prefill(vo, W, orc, args))
+        torch.cuda.empty_cache()
+        line["cfg4"] = nested_record(bench_model(vo, W, orc, args))
         lines.append(line)
     elif args.config in ("cfg2", "all"):
         lines.append(bench_decode(vo, W, orc, args, cfg2))
