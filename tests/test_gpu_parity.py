@@ -253,32 +253,42 @@ def test_decode_streaming_loads_bitwise_equal(vo, monkeypatch):
         _assert_close(got, want, f"streaming shared={shared}")
 
 
-@pytest.mark.parametrize("hd,heads,kvh,split,waves,mode,nalias", [
+_PACK_CASES = [
     (128, 64, 8, "1024", "4", 1, 12),  # cfg5's shape: group 8, two rows per item
-    (128, 64, 8, "1024", "4", 2, 12),  # shared packs: 4 wavefronts x 2 rows
-    (128, 64, 8, "2048", "4", 2, 2),   # a shared pack of 2 of its 8 rows
+    (128, 64, 8, "1024", "4", 2, 12),  # shared packs: 2 rows per tile
+    (128, 64, 8, "2048", "4", 2, 2),   # a shared pack of 2 rows
     (128, 64, 8, "2048", "4", 2, 1),   # no two rows share a split: nothing packed
+    (128, 64, 8, "64", "4", 2, 12),    # 2 chunks per split: states 2 and 3 stay empty
+    (128, 64, 8, "96", "4", 2, 12),    # 3 chunks: the pairs' last step has one chunk
     (128, 32, 8, "512", "1", 1, 12),   # group 4, four rows per item, no LDS merge
     (128, 32, 8, "512", "1", 2, 12),   # one wavefront: shared packs fall back to one tile
     (128, 32, 8, "512", "8", 2, 12),   # 8 wavefronts: shared packs fall back to one tile
-    (128, 32, 8, "512", "4", 2, 12),   # 4 wavefronts x 4 rows: one pack of 12 of 16 rows
+    (128, 32, 8, "512", "4", 2, 12),   # 4 rows per tile: a short last pack
     (64, 6, 2, "256", "2", 1, 12),     # group 3, five rows per item, a short last pack
-    (64, 6, 2, "256", "4", 2, 12),     # group 3, shared: 4 wavefronts x 5 rows
-])
+    (64, 6, 2, "256", "4", 2, 12),     # group 3, shared: 5 rows per tile
+]
+
+
+@pytest.mark.parametrize("hd,heads,kvh,split,waves,mode,nalias,pairs",
+                         [c + ("1",) for c in _PACK_CASES] +
+                         [c + ("0",) for c in _PACK_CASES if c[5] == 2 and c[4] == "4"])
 def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, waves, mode,
-                                    nalias):
+                                    nalias, pairs):
     """Rows whose full splits read the same physical blocks (an aliased
     prefix) share one work item, each row in its own head columns: one
-    16-column MFMA tile per item (VO_DECODE_PACK=1), or a shared pack whose 4
-    wavefronts each take a tile over chunks staged once in LDS (=2, the
-    default).  The outputs are bitwise those of the unpacked plan
-    (VO_DECODE_PACK=0) and within tolerance of the oracle; the plan really
-    packs: each of the two shared prefix splits of the aliasing rows runs as
-    ceil(rows / P) items, with P rows per item for the mode."""
+    16-column MFMA tile per item (VO_DECODE_PACK=1), or a shared pack over
+    chunks staged once in LDS (=2, the default) whose tiles have two
+    wavefronts each, one per pair of softmax states (VO_DECODE_SHARED_PAIRS=1,
+    the default), or one wavefront each (=0).  The outputs are bitwise those
+    of the unpacked plan (VO_DECODE_PACK=0) and within tolerance of the
+    oracle; the plan really packs: each of the two shared prefix splits of the
+    aliasing rows runs as ceil(rows / P) items, with P rows per item for the
+    mode."""
     monkeypatch.setenv("VO_DECODE_SPLIT", split)
     monkeypatch.setenv("VO_DECODE_WAVES", waves)
+    monkeypatch.setenv("VO_DECODE_SHARED_PAIRS", pairs)
     _say(f"decode row packing hd={hd} heads={heads} kvh={kvh} split={split} waves={waves} "
-         f"mode={mode} aliasing rows={nalias}")
+         f"mode={mode} aliasing rows={nalias} pairs={pairs}")
     L = int(split)
     backend = vo.HipBackend(device=0, max_seqs=64, max_rows=W.FILL_ROWS, max_table_entries=8192,
                             max_query_heads=heads)
@@ -295,7 +305,7 @@ def test_decode_row_packing_bitwise(vo, monkeypatch, hd, heads, kvh, split, wave
     if mode == 1:
         P = one_tile
     else:
-        P = 4 * (16 // group)
+        P = (2 if pairs == "1" else 4) * (16 // group)
         if min(P, len(extra)) < 2:
             P = 1  # nothing to share
     parts = sum(-(-(c + 1) // L) for c in ctx)
@@ -784,9 +794,9 @@ def test_decode_shared_packs_pool_at_and_past_4_gib(vo, num_blocks):
                  block_size=16, num_blocks=num_blocks, context_lens=ctx, seed=72,
                  shared_prefix=shared, shared_count=8, tables=tables)
     out = _out(wl, backend)
-    # 8 rows x 3 splits + 5 for the long row; the 8 rows' two prefix splits
-    # run as one shared pack each.
-    assert backend.step_meta(wl.pool).decode_plan() == (29 - 2 * 7, 29, 8)
+    # 8 rows x 3 splits + 5 for the long row; each of the 8 rows' two prefix
+    # splits runs as two shared packs of 4 rows.
+    assert backend.step_meta(wl.pool).decode_plan() == (29 - 2 * 6, 29, 4)
     _assert_close(out.float().cpu().numpy(), _oracle_renumbered(vo, wl),
                   f"decode shared packs on a {num_blocks}-block pool")
     del wl, out

@@ -528,6 +528,254 @@ __device__ __forceinline__ void shared_split(
     }
 }
 
+// A shared pack in wavefront pairs.  The same staged chunks and the same
+// four softmax states as shared_split, but each 16-column tile has two
+// wavefronts: the one of parity 0 keeps states 0 and 2 (chunks 4k and
+// 4k + 2), the one of parity 1 states 1 and 3 (chunks 4k + 1, 4k + 3).  One
+// step stages two chunks (2j in stage 2(j % 2), 2j + 1 in the next) and each
+// wavefront of a pair computes one of them, so a wavefront walks half of the
+// split's chunks.  The workgroup holds W / 2 tiles, so a pack has W / 2 *
+// (16 / G) rows.  Every state still takes its chunks in increasing order,
+// and the four states are merged in the order 0..3 with the register path's
+// arithmetic, so a row's bits are the register path's, as in shared_split.
+// Two chunks are consumed per step, so the DMA of a step's pair is issued
+// one step ahead (the four stages hold two pairs).
+template <int HD, int W>
+__device__ __forceinline__ void shared_split_pairs(
+    const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
+    uint32_t kvh, uint32_t item, const u32x4 rec, const uint32_t *__restrict__ tables,
+    const uint32_t *__restrict__ row_info, uint32_t split_keys, const uint16_t *__restrict__ q,
+    uint16_t *__restrict__ out, float *__restrict__ part_acc, float *__restrict__ part_ml,
+    uint32_t num_heads, uint32_t group, float scale_log2, const uint32_t *__restrict__ mates,
+    uint32_t pack, uint8_t *__restrict__ st0, uint8_t *__restrict__ st1,
+    uint8_t *__restrict__ st2, uint8_t *__restrict__ st3) {
+#pragma clang fp contract(off)  // the merge below rounds as the register path's does
+    constexpr int KK = HD / 32;
+    constexpr int DT = HD / 16;
+    using S = SharedStage<HD>;
+    constexpr uint32_t kTile = kBS * HD;
+    constexpr int NI = S::BYTES / 1024 / W;  // DMA instructions per wavefront and chunk
+    static_assert(W == 4 && S::BYTES % (1024 * W) == 0 && 2 * NI <= 15, "chunk DMA split");
+    constexpr uint32_t KIB_PER_TILE = S::TB / 1024;
+    constexpr uint32_t kTiles = W / 2;
+    // The partner's two states go through the stages: per tile, DT x 64
+    // lanes of floatx4 per state (one stage), and (m, l) per state and lane.
+    static_assert(2 * DT * 64 * 16 <= S::BYTES && kTiles * 4 * 64 * 4 <= S::BYTES,
+                  "pair exchange fits the stages");
+
+    const uint32_t row = uniform_u32(rec[0]);
+    const uint32_t split = uniform_u32(rec[1]);
+    const uint32_t *table = tables + uniform_u32(rec[2]);
+    const uint32_t nchunks = split_keys / kChunk;  // a full split
+    constexpr int TV = kMaxSplitKeys / kBS / 64;
+    const uint32_t nblk = 2 * nchunks;
+    uint32_t tv[TV];
+#pragma unroll
+    for (int k = 0; k < TV; ++k) {
+        const uint32_t i = 64 * k + static_cast<uint32_t>(threadIdx.x & 63);
+        tv[k] = i < nblk ? table[i] : 0u;
+    }
+    auto block_id = [&](uint32_t i) {  // i < nblk, wave-uniform
+        uint32_t b = __builtin_amdgcn_readlane(tv[0], i & 63);
+#pragma unroll
+        for (int k = 1; k < TV; ++k) {
+            const uint32_t bk = __builtin_amdgcn_readlane(tv[k], i & 63);
+            b = (i >> 6) == static_cast<uint32_t>(k) ? bk : b;
+        }
+        return b;
+    };
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane & 15;
+    const int g = lane >> 4;
+    const uint32_t tile = static_cast<uint32_t>(wave) >> 1;
+    const uint32_t par = static_cast<uint32_t>(wave) & 1;
+
+    // This tile's columns: row slot tile * R + h / G, head h % G, with
+    // R = ceil(pack / tiles) <= 16 / G rows per tile.
+    const uint32_t per_tile = (pack + kTiles - 1) / kTiles;
+    const uint32_t hslot = static_cast<uint32_t>(h) / group;
+    const uint32_t pslot = tile * per_tile + hslot;
+    const uint32_t hh = static_cast<uint32_t>(h) - hslot * group;
+    uint32_t crow = kNoMate;
+    if (hslot < per_tile) {
+        if (pslot == 0)
+            crow = row;
+        else if (pslot < pack)
+            crow = mates[(pack - 1) * item + pslot - 1];
+    }
+    const bool head_ok = crow != kNoMate;
+    const bool wave_live = __builtin_amdgcn_ballot_w64(head_ok) != 0;
+    const uint32_t qhead = kvh * group + hh;
+    bf16x8 qv[KK];
+    {
+        const uint16_t *qp = q + (static_cast<uint64_t>(head_ok ? crow : row) * num_heads + qhead) * HD + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) qv[kk] = head_ok ? load_bf16x8(qp + 32 * kk) : bf16x8{};
+    }
+    u32x2 cinfo = {0u, 0u};
+    if (head_ok) cinfo = *reinterpret_cast<const u32x2 *>(row_info + 2 * static_cast<uint64_t>(crow));
+
+    // DMA as in shared_split: instruction i of wavefront w copies KiB i * W
+    // + w of a chunk's stage.
+    uint32_t dma_off[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const uint32_t qi = static_cast<uint32_t>(i * W + wave);
+        const uint32_t t = qi / KIB_PER_TILE;
+        const uint32_t u = (qi % KIB_PER_TILE) * 64 + lane;
+        dma_off[i] = 16 * (t < 2 ? S::swz_k(u, t) : S::swz_v(u));
+    }
+    const uint64_t block_stride = static_cast<uint64_t>(kv_heads) * kTile;
+    auto dma_chunk = [&](uint8_t *stage, uint32_t c) {
+        const uint32_t b0 = block_id(2 * c);
+        const uint32_t b1 = block_id(2 * c + 1);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t qi = static_cast<uint32_t>(i * W + wave);
+            const uint32_t t = qi / KIB_PER_TILE;
+            const uint16_t *pool = t < 2 ? k_pool : v_pool;
+            const uint32_t blk = (t & 1) ? b1 : b0;
+            dma16(pool + static_cast<uint64_t>(blk) * block_stride + static_cast<uint64_t>(kvh) * kTile,
+                  S::TB, stage + qi * 1024, dma_off[i]);
+        }
+    };
+
+    // LDS read offsets: shared_split's.
+    const uint32_t m = static_cast<uint32_t>(h);
+    const uint32_t kb_hi = m >= 8 ? 1u : 0u;
+    const uint32_t kx = (8 * ((m >> 2) & 1) + (m & 3)) * 4 + static_cast<uint32_t>(g);
+    const uint32_t k_rd = kb_hi * S::TB + 16 * S::swz_k(kx, kb_hi);
+    const uint32_t vb_hi = g >= 2 ? 1u : 0u;
+    const uint32_t vx = 2 * m + static_cast<uint32_t>(g & 1);
+    const uint32_t v_rd = (2 + vb_hi) * S::TB + 16 * S::swz_v(vx);
+
+    // Local state i is state par + 2 i.
+    float ms[2], ls[2];
+    floatx4 as[2][DT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        ms[i] = -INFINITY;
+        ls[i] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) as[i][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto compute = [&](const uint8_t *cur, int i) __attribute__((always_inline)) {
+        bf16x8 ka[KK], kb[KK], va[DT];
+        floatx4 sa0, sa1;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            ka[kk] = *reinterpret_cast<const bf16x8 *>(cur + k_rd + 1024 * kk);
+            kb[kk] = *reinterpret_cast<const bf16x8 *>(cur + k_rd + 1024 * kk + 256);
+        }
+        chunk_qk<HD>(ka, kb, qv, sa0, sa1);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) va[dt] = *reinterpret_cast<const bf16x8 *>(cur + v_rd + 512 * dt);
+        chunk_update<HD>(sa0, sa1, va, false, 8, scale_log2, ms[i], ls[i], as[i]);
+    };
+    // Step j: wait for chunks 2j and 2j + 1 (the only DMA in flight), then
+    // for every wavefront to be done with step j - 1's pair, refill that
+    // pair with chunks 2j + 2 and 2j + 3, and compute chunk 2j + par into
+    // local state j % 2 (state (2j + par) % 4).  Each stage is named in its
+    // own branch, so that the compiler tells the stage being read from the
+    // ones the DMA fills.  Every step issues its DMA (past the last chunk
+    // the block ids repeat the split's last blocks).
+    auto step = [&](auto s_pair, uint32_t j) __attribute__((always_inline)) {
+        constexpr int sp = decltype(s_pair)::value;
+        wait_barrier<0>();
+        dma_chunk(sp ? st0 : st2, min(2 * j + 2, nchunks - 1));
+        dma_chunk(sp ? st1 : st3, min(2 * j + 3, nchunks - 1));
+        if (!wave_live || 2 * j + par >= nchunks) return;
+        if (par == 0)
+            compute(sp ? st2 : st0, sp);
+        else
+            compute(sp ? st3 : st1, sp);
+    };
+    const uint32_t nsteps = (nchunks + 1) / 2;
+    dma_chunk(st0, 0);
+    dma_chunk(st1, min(1u, nchunks - 1));
+    for (uint32_t j = 0; j < nsteps; j += 2) {
+        step(std::integral_constant<int, 0>{}, j);
+        if (j + 1 >= nsteps) break;
+        step(std::integral_constant<int, 1>{}, j + 1);
+    }
+    // The DMA past the last chunk must land before the stages are reused.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    // The running sums are per lane group (the four lanes of a column are
+    // all live or all not).
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        ls[i] += __shfl_xor(ls[i], 16, 64);
+        ls[i] += __shfl_xor(ls[i], 32, 64);
+    }
+    // The parity-1 wavefront hands its states to its partner through the
+    // stages, once every wavefront is done reading them.
+    __syncthreads();
+    floatx4 *xa = reinterpret_cast<floatx4 *>(tile == 0 ? st0 : st1);  // [2][DT][64]
+    float *xml = reinterpret_cast<float *>(st2) + tile * 4 * 64;     // [2][m, l][64]
+    if (par == 1 && head_ok) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) xa[(i * DT + dt) * 64 + lane] = as[i][dt];
+            xml[(2 * i) * 64 + lane] = ms[i];
+            xml[(2 * i + 1) * 64 + lane] = ls[i];
+        }
+    }
+    __syncthreads();
+    if (par == 1 || !head_ok) return;
+
+    // The register path's merge of its W = 4 wavefronts' states, in order
+    // 0..3: state 2i is this wavefront's local state i, state 2i + 1 the
+    // partner's.
+    float sm[4], sl[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        sm[2 * i] = ms[i];
+        sl[2 * i] = ls[i];
+        sm[2 * i + 1] = xml[(2 * i) * 64 + lane];
+        sl[2 * i + 1] = xml[(2 * i + 1) * 64 + lane];
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm[w]);
+    float den = 0.0f;
+    floatx4 num[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) num[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float mw = sm[w];
+        if (mw != -INFINITY) {
+            const float e = __builtin_amdgcn_exp2f(mw - mx);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const floatx4 a = (w & 1) ? xa[((w >> 1) * DT + dt) * 64 + lane] : as[w >> 1][dt];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) num[dt][j] += e * a[j];
+            }
+            den += e * sl[w];
+        }
+    }
+    if (cinfo[1] == 1) {
+        uint16_t *op = out + static_cast<uint64_t>(crow) * num_heads * HD +
+                       static_cast<uint64_t>(qhead) * HD + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) op[16 * dt + j] = f32_to_bf16_bits(num[dt][j] / den);
+    } else {
+        const uint64_t part = static_cast<uint64_t>(cinfo[0] + split) * num_heads + qhead;
+        float *ap = part_acc + part * HD + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<floatx4 *>(ap + 16 * dt) = num[dt];
+        if (g == 0) {
+            part_ml[2 * part] = mx;
+            part_ml[2 * part + 1] = den;
+        }
+    }
+}
+
 template <int HD, int W, bool NT>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2))) void
 decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool,
@@ -540,7 +788,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
                      const uint32_t *__restrict__ mates, uint32_t pack, uint16_t *__restrict__ k_w,
                      uint16_t *__restrict__ v_w, const uint16_t *__restrict__ new_k,
                      const uint16_t *__restrict__ new_v, const uint32_t *__restrict__ new_slots,
-                     uint32_t num_shared) {
+                     uint32_t num_shared, uint32_t shared_pairs) {
 #pragma clang fp contract(off)  // the wavefronts' merge rounds as a shared pack's does
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
@@ -551,7 +799,7 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     // compiler can tell one stage's DMA from another stage's reads and waits
     // for neither); the register path's merge keeps wavefront w's
     // accumulators in stage w.
-    constexpr bool kStages = W == kSharedWaves && !NT;
+    constexpr bool kStages = W == kSharedWaves;
     constexpr uint32_t kStageBytes = kStages ? SharedStage<HD>::BYTES : 16;
     __shared__ __align__(1024) uint8_t sh0[kStageBytes];
     __shared__ __align__(1024) uint8_t sh1[kStageBytes];
@@ -582,9 +830,15 @@ decode_splitk_kernel(const uint16_t *__restrict__ k_pool, const uint16_t *__rest
     }
     if constexpr (kStages) {
         if (item < num_shared) {
-            shared_split<HD, W>(k_pool, v_pool, kv_heads, kvh, item, rec, tables, row_info,
-                                split_keys, q, out, part_acc, part_ml, num_heads, group,
-                                scale_log2, mates, pack, sh0, sh1, sh2, sh3);
+            if (shared_pairs)
+                shared_split_pairs<HD, W>(k_pool, v_pool, kv_heads, kvh, item, rec, tables,
+                                          row_info, split_keys, q, out, part_acc, part_ml,
+                                          num_heads, group, scale_log2, mates, pack, sh0, sh1,
+                                          sh2, sh3);
+            else
+                shared_split<HD, W>(k_pool, v_pool, kv_heads, kvh, item, rec, tables, row_info,
+                                    split_keys, q, out, part_acc, part_ml, num_heads, group,
+                                    scale_log2, mates, pack, sh0, sh1, sh2, sh3);
             return;
         }
     }
@@ -893,15 +1147,16 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
     // Shared packs: W wavefronts of up to 16 / G rows; the other items then
     // carry no mates.  (A shared pack never holds a row's new key: its blocks
     // are read by another row, so a plan with new keys has none there.)
-    if (shared != 0 && (W != kSharedWaves || NT || group > 16 || pack > W * (16 / group) ||
-                        plan.split_keys % kChunk != 0))
+    const uint32_t shared_tiles = plan.shared_pairs ? W / 2 : W;
+    if (shared != 0 && (W != kSharedWaves || group > 16 ||
+                        pack > shared_tiles * (16 / group) || plan.split_keys % kChunk != 0))
         return hipErrorInvalidValue;
     const uint32_t item_pack = shared ? 1u : pack;
     if (item_pack * group > 16 || (pack > 1 && plan.mates == nullptr)) return hipErrorInvalidValue;
     // With 4 wavefronts (not streaming) the merge lives in the shared-pack
     // stages (at most 16 columns of HD floats per wavefront, 8 KiB at
     // head_dim 128).
-    constexpr bool kStages = W == kSharedWaves && !NT;
+    constexpr bool kStages = W == kSharedWaves;
     const size_t smem =
         (W == 1 || kStages) ? 0
                             : (2 * W * 16 + static_cast<size_t>(W) * item_pack * group * kAccStride<HD>) * 4;
@@ -914,7 +1169,7 @@ hipError_t launch_split(const PoolLayer &pool, const MetaView &meta, const Decod
                        plan.split_keys, q, out, plan.part_acc, plan.part_ml, num_heads, group,
                        scale_log2, plan.counts, plan.mates, pack, pool.k, pool.v,
                        nkeys ? nkeys->k : nullptr, nkeys ? nkeys->v : nullptr,
-                       nkeys ? nkeys->slots : nullptr, shared);
+                       nkeys ? nkeys->slots : nullptr, shared, plan.shared_pairs ? 1u : 0u);
     return hipGetLastError();
 }
 

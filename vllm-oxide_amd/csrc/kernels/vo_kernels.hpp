@@ -180,6 +180,10 @@ struct DecodePlan {
     // 16 / group rows each, so pack <= W * (16 / group); every other item
     // then has no mates.  0: no shared packs.
     uint32_t num_shared;
+    // Shared packs in wavefront pairs: two wavefronts per 16-column tile,
+    // each keeping two of the tile's four softmax states, so pack <= W / 2 *
+    // (16 / group) and each wavefront walks half of the split's chunks.
+    bool shared_pairs;
 };
 
 constexpr uint32_t kNoMate = 0xffffffffu;

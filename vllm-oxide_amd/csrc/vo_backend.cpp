@@ -417,9 +417,22 @@ uint32_t decode_shared_rows(const vo_step_meta *m, uint32_t waves) {
     return p >= 2 ? static_cast<uint32_t>(p) : 1u;
 }
 
+// The mates buffer is sized for the larger packs (one wavefront per tile),
+// whichever form a later plan takes.
 uint32_t decode_pack_limit(const vo_step_meta *m) {
     return std::max(decode_pack_rows(m, 1), decode_shared_rows(m, 4));
 }
+
+// Shared packs in wavefront pairs (two wavefronts per tile, each walking
+// half of the split's chunks; half the rows per pack).  VO_DECODE_SHARED_PAIRS
+// = 0 keeps one wavefront per tile (a tuning knob, read per plan).
+bool decode_shared_pairs() { return env_int("VO_DECODE_SHARED_PAIRS", 1) != 0; }
+
+// With shared packs, the blocks several rows read go through the packs'
+// LDS stages, so the other items stream their (mostly private) blocks with
+// non-temporal loads, which keeps the shared blocks in L2 for the packs.
+// VO_DECODE_PACK_NT = 0 keeps cached loads (a tuning knob, read per plan).
+bool decode_pack_nt() { return env_int("VO_DECODE_PACK_NT", 1) != 0; }
 
 uint32_t decode_pack_mode() {
     const int v = env_int("VO_DECODE_PACK", kPackShared);
@@ -555,12 +568,14 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
     // Shared packs need 4 wavefronts (the kernel keeps one softmax state per
     // wavefront in registers and stages four chunks).
     if (mode == kPackShared && waves != 4) mode = kPackOneTile;
+    const bool pairs = mode == kPackShared && decode_shared_pairs();
     uint32_t P = mode == kPackOff      ? 1u
-                 : mode == kPackShared ? decode_shared_rows(m, static_cast<uint32_t>(waves))
+                 : mode == kPackShared ? decode_shared_rows(m, static_cast<uint32_t>(pairs ? waves / 2 : waves))
                                        : decode_pack_rows(m, 1);
     uint32_t *mates = nullptr;
     m->plan.mates = nullptr;
     m->plan.num_shared = 0;
+    m->plan.shared_pairs = pairs;
     if (P > 1) {
         mates = pk.add(kRegMates, (P - 1) * parts, &dp);
         m->plan.mates = dp;
@@ -636,7 +651,7 @@ vo_status plan_decode_rows(vo_step_meta *m, Packer &pk, const std::vector<uint32
         m->plan.launch_work = static_cast<uint32_t>(m->fixed.work_cap);
         m->plan.launch_reduce = static_cast<uint32_t>(m->fixed.seqs);
     } else {
-        m->plan.streaming = streaming;
+        m->plan.streaming = streaming || (m->plan.num_shared != 0 && decode_pack_nt());
         m->plan.launch_work = static_cast<uint32_t>(num_work);
         m->plan.launch_reduce = static_cast<uint32_t>(nred);
     }
