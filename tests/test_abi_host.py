@@ -148,3 +148,27 @@ def test_metadata_errors_match_oracle(vo):
         if got_err is not None:
             assert (got_err.seq, got_err.tokens, got_err.needed, got_err.have) == (
                 want_err.seq, want_err.tokens, want_err.needed, want_err.have)
+
+
+def test_step_metas_are_immutable(vo):
+    """A PrefillMeta / DecodeMeta holds read-only copies of its arrays and
+    rejects attribute assignment, so HipBackend's one upload per meta object
+    cannot go stale; a changed step is a new object (dataclasses.replace)."""
+    import dataclasses
+    table = np.array([3, 1], np.uint32)
+    pm = vo.PrefillMeta.new([vo.PrefillSeq(5, 4, table)], 16)
+    dm = vo.DecodeMeta.new([vo.DecodeSeq(20, table)], 16)
+    table[0] = 7  # the caller's array is not the meta's
+    assert pm.block_tables[0][0] == 3 and dm.block_tables[0][0] == 3
+    for meta in (pm, dm):
+        for name in ("positions", "slot_mapping", "row_seq", "row_num_keys"):
+            with pytest.raises(ValueError):
+                getattr(meta, name)[0] = 1
+        with pytest.raises(ValueError):
+            meta.block_tables[0][0] = 1
+        with pytest.raises(dataclasses.FrozenInstanceError):
+            meta.positions = np.zeros(1, np.uint32)
+    changed = dataclasses.replace(pm, slot_mapping=[80, 81, 82, 83])
+    assert changed is not pm and list(changed.slot_mapping) == [80, 81, 82, 83]
+    assert not changed.slot_mapping.flags.writeable
+

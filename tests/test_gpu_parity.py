@@ -7,6 +7,7 @@ Bars:
 Plus size-independent properties at full BASELINE sizes: batch invariance and
 block-relabelling invariance (bitwise), single key -> V exactly.
 """
+import dataclasses
 import os
 
 import numpy as np
@@ -1103,8 +1104,8 @@ def test_rope_write_kv_repeated_slot_rotates_every_q_row(vo, gpu_backend):
     table = vo.RopeTable(hd, 500000.0, 64)
     layout = vo.KvLayout(1, 8, 16, kvh, hd)
     pool = gpu_backend.alloc_kv_pool(layout)
-    meta = vo.PrefillMeta.new([vo.PrefillSeq(0, 3, [5])], 16)
-    meta.slot_mapping[:] = [80, 81, 80]
+    meta = dataclasses.replace(vo.PrefillMeta.new([vo.PrefillSeq(0, 3, [5])], 16),
+                               slot_mapping=[80, 81, 80])
     g = torch.Generator(device="cuda:0")
     g.manual_seed(9)
     q = torch.randn((3, heads * hd), generator=g, device="cuda:0").to(torch.bfloat16)

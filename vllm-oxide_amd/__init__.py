@@ -372,9 +372,21 @@ def _csr(tables: List[np.ndarray]):
     return off, flat
 
 
-@dataclass
+def _frozen(a, dtype) -> np.ndarray:
+    """A read-only copy of `a` as a flat array of `dtype`."""
+    out = np.array(a, dtype=dtype, copy=True).reshape(-1)
+    out.setflags(write=False)
+    return out
+
+
+@dataclass(frozen=True)
 class PrefillMeta:
-    """paged.rs:97-114, built by the library's PrefillMeta::new restatement."""
+    """paged.rs:97-114, built by the library's PrefillMeta::new restatement.
+
+    Immutable: every array is a read-only copy, so a meta object names one
+    step's contents and HipBackend may upload it once for all the layers
+    that receive it.  A changed step is a new object
+    (``dataclasses.replace``)."""
     block_size: int
     block_tables: List[np.ndarray]
     context_lens: np.ndarray
@@ -384,6 +396,16 @@ class PrefillMeta:
     row_seq: np.ndarray
     row_num_keys: np.ndarray
     kind: str = field(default="prefill", repr=False)
+
+    def __post_init__(self):
+        put = object.__setattr__
+        put(self, "block_tables", tuple(_frozen(t, np.uint32) for t in self.block_tables))
+        put(self, "context_lens", _frozen(self.context_lens, np.uint64))
+        put(self, "seq_row_starts", _frozen(self.seq_row_starts, np.uint64))
+        put(self, "positions", _frozen(self.positions, np.uint32))
+        put(self, "slot_mapping", _frozen(self.slot_mapping, np.uint32))
+        put(self, "row_seq", _frozen(self.row_seq, np.uint64))
+        put(self, "row_num_keys", _frozen(self.row_num_keys, np.uint64))
 
     @staticmethod
     def new(seqs: Sequence[PrefillSeq], block_size: int) -> "PrefillMeta":
@@ -417,9 +439,10 @@ class PrefillMeta:
         return out[: self.num_seqs()]
 
 
-@dataclass
+@dataclass(frozen=True)
 class DecodeMeta:
-    """paged.rs:173-186, built by the library's DecodeMeta::new restatement."""
+    """paged.rs:173-186, built by the library's DecodeMeta::new restatement.
+    Immutable, as PrefillMeta."""
     block_size: int
     block_tables: List[np.ndarray]
     positions: np.ndarray
@@ -427,6 +450,14 @@ class DecodeMeta:
     row_seq: np.ndarray
     row_num_keys: np.ndarray
     kind: str = field(default="decode", repr=False)
+
+    def __post_init__(self):
+        put = object.__setattr__
+        put(self, "block_tables", tuple(_frozen(t, np.uint32) for t in self.block_tables))
+        put(self, "positions", _frozen(self.positions, np.uint32))
+        put(self, "slot_mapping", _frozen(self.slot_mapping, np.uint32))
+        put(self, "row_seq", _frozen(self.row_seq, np.uint64))
+        put(self, "row_num_keys", _frozen(self.row_num_keys, np.uint64))
 
     @staticmethod
     def new(seqs: Sequence[DecodeSeq], block_size: int) -> "DecodeMeta":
@@ -890,6 +921,8 @@ class HipBackend:
         return m
 
     def _meta_for(self, pool: KvPool, meta, stream, slot: str = "step") -> StepMeta:
+        # A PrefillMeta / DecodeMeta is immutable, so the object names its
+        # contents: the step's upload serves every layer that receives it.
         m = self.step_meta(pool, slot)
         if m.holds is not meta:
             m.upload(meta, stream)
