@@ -572,31 +572,35 @@ def test_prefill_chunked_with_context(vo, gpu_backend, hd, heads, kvh):
     _assert_close(out.float().cpu().numpy(), want, f"prefill hd={hd}")
 
 
+@pytest.mark.parametrize("pipe", ["1", "0"])
 @pytest.mark.parametrize("offset", ["fixed", "running"])
-def test_prefill_64_row_workgroups_edge_shapes(vo, gpu_backend, monkeypatch, offset):
-    """The 64-row workgroups at GQA 4, head_dim 128, with the fixed tile-0
-    softmax offset and with the running max (VO_PREFILL_OFFSET), on a grid
-    small enough that the 32-row workgroups would otherwise serve it
-    (VO_PREFILL_NARROW=0): chunks starting at 0, mid-block, on and next to
-    tile boundaries; items of 2, 31, 32, 33, 64 and 65 rows; one row per
-    block of a 2047-key context."""
-    _say(f"prefill 64-row workgroups ({offset} offset)")
+def test_prefill_64_row_workgroups_edge_shapes(vo, gpu_backend, monkeypatch, offset, pipe):
+    """The 64-row workgroups at GQA 4, head_dim 128 -- the pipelined
+    4-wavefront kernel and the 8-wavefront one (VO_PREFILL_PIPE=0) -- with
+    the fixed tile-0 softmax offset and with the running max
+    (VO_PREFILL_OFFSET), on a grid small enough that the 32-row workgroups
+    would otherwise serve it (VO_PREFILL_NARROW=0): chunks starting at 0,
+    mid-block, on and next to tile boundaries; items of 2, 31, 32, 33, 64
+    and 65 rows; one row per block of a 2047-key context."""
+    _say(f"prefill 64-row workgroups ({offset} offset, pipe {pipe})")
     monkeypatch.setenv("VO_PREFILL_NARROW", "0")
     monkeypatch.setenv("VO_PREFILL_OFFSET", offset)
+    monkeypatch.setenv("VO_PREFILL_PIPE", pipe)
     wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
                  block_size=16, num_blocks=1200,
                  context_lens=[0, 5, 63, 64, 65, 1000, 2047, 31],
                  num_new=[2, 31, 32, 33, 64, 65, 129, 200], seed=61)
     gpu_backend.step_meta(wl.pool).holds = None
     out, ran = _out_with_prefill_instances(vo, wl, gpu_backend)
-    assert ran == {"prefill_dma"}, ran  # the setting is honoured: 64-row workgroups ran
+    # the settings are honoured: 64-row workgroups of the chosen kernel ran
+    assert ran == ({"prefill_pipe"} if pipe == "1" else {"prefill_dma"}), ran
     want = W.oracle_attention(orc, wl)
     _assert_close(out.float().cpu().numpy(), want, f"prefill 64-row workgroups ({offset})")
 
 
-@pytest.mark.parametrize("narrow", ["1", "0"])
+@pytest.mark.parametrize("narrow,pipe", [("1", "1"), ("0", "1"), ("0", "0")])
 @pytest.mark.parametrize("factor", [4.0, 10.0])
-def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, factor):
+def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, pipe, factor):
     """The prefill kernel first keeps each row's tile-0 max as its softmax
     offset.  Key 200 of sequence 0 (cached, KV tile 3) is set to factor x
     query row 0's head-0 vector (KV head 0 serves heads 0..3), so that row's
@@ -604,10 +608,12 @@ def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, f
     at factor 4 (row sum past the 2^40 bound, no overflow yet) and ~163 at
     factor 10, where 2^163 overflows f32 and only the recompute with the
     running max gives finite output.  Every row must match the oracle, in
-    32-row (narrow) and 64-row workgroups."""
+    32-row (narrow) and 64-row workgroups (the pipelined kernel and the
+    8-wavefront one)."""
     import torch
-    _say(f"prefill key far above tile-0 max (factor {factor}, narrow {narrow})")
+    _say(f"prefill key far above tile-0 max (factor {factor}, narrow {narrow}, pipe {pipe})")
     monkeypatch.setenv("VO_PREFILL_NARROW", narrow)
+    monkeypatch.setenv("VO_PREFILL_PIPE", pipe)
     ctx, new = [300, 0, 900], [64, 128, 100]
     wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
                  block_size=16, num_blocks=200, context_lens=ctx, num_new=new, seed=62)
@@ -622,7 +628,8 @@ def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, f
     wl.host["ctx"][0] = (keys.float().cpu().numpy(), wl.host["ctx"][0][1])
     gpu_backend.step_meta(wl.pool).holds = None
     out, ran = _out_with_prefill_instances(vo, wl, gpu_backend)
-    assert ran == ({"prefill_dma_narrow"} if narrow == "1" else {"prefill_dma"}), ran
+    assert ran == ({"prefill_dma_narrow"} if narrow == "1"
+                   else {"prefill_pipe"} if pipe == "1" else {"prefill_dma"}), ran
     want = W.oracle_attention(orc, wl)
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
@@ -817,6 +824,34 @@ def test_prefill_cfg3_full_size_sampled_rows(vo, gpu_backend):
     rows = np.unique(np.concatenate([np.arange(0, wl.rows, 29), starts[1:] - 1, starts[:-1]]))
     want = W.oracle_attention(orc, wl, rows=rows)
     _assert_close(out[rows], want, "cfg3")
+
+
+@pytest.mark.parametrize("case", ["cfg3", "edges"])
+def test_prefill_pipe_kernel_bitwise_equals_dma_kernel(vo, gpu_backend, monkeypatch, case):
+    """The pipelined 4-wavefront kernel computes each row with the 32-row
+    kernels' operations in their order, so its output is bitwise the
+    8-wavefront DMA kernel's (VO_PREFILL_PIPE=0): at BASELINE config 3's full
+    size, and on items that end before, at and past tile and 32-row-group
+    boundaries (so that the pipelined loop runs 0, 1, 2 and many tiles and
+    the masked tiles follow it in either S buffer)."""
+    _say(f"prefill pipelined kernel vs DMA kernel bitwise ({case})")
+    monkeypatch.setenv("VO_PREFILL_NARROW", "0")
+    if case == "cfg3":
+        ctx, new = W.cfg3_context_lens(), [512] * 8
+        nb = 12000
+    else:
+        ctx = [0, 63, 64, 127, 128, 130, 191, 192, 255, 1000, 3001, 4095]
+        new = [64, 1, 65, 2, 64, 31, 33, 1, 129, 40, 77, 64]
+        nb = 1200
+    wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
+                 block_size=16, num_blocks=nb, context_lens=ctx, num_new=new, seed=71)
+    outs = {}
+    for pipe in ("1", "0"):
+        monkeypatch.setenv("VO_PREFILL_PIPE", pipe)
+        out, ran = _out_with_prefill_instances(vo, wl, gpu_backend)
+        assert ran == ({"prefill_pipe"} if pipe == "1" else {"prefill_dma"}), ran
+        outs[pipe] = out.clone()
+    assert np.array_equal(_bits(outs["1"]), _bits(outs["0"]))
 
 
 MIXED_CTX = [0, 1, 15, 16, 17, 63, 64, 65, 700, 1023, 1024, 1025, 3000, 0, 100, 700, 5, 2047]

@@ -103,6 +103,27 @@ __device__ __forceinline__ float sum8(bf16x8 v, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
 }
 
+__device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Row sums on the matrix core.  The P operand of the P.V MFMA (32 rows x 16
+// keys: lane l holds 8 keys of row l % 32) fed as the B operand of
+// v_mfma_f32_16x16x32_bf16 makes lane l's 8 values the 32-deep column
+// l % 16's k-slice of lane group g = l / 16.  With every value of A-lane
+// a = 16 g + m set to 1 when g and m / 4 have the same parity (else 0),
+// output element (m, n) adds the 8-value slices of B-lanes n + 16 g over
+// the groups g with g % 2 == (m / 4) % 2: both key halves of row
+// n + 16 ((m / 4) % 2).  Output lane l holds rows m = 4 (l / 16) + r of
+// column l % 16, so all four of its values are the sum of its own row
+// l % 32.  Eight v_dot2c per 16 keys would block the MFMA pipe (a dot
+// instruction does not co-issue with MFMAs on gfx950); this takes one
+// 16-cycle MFMA.
+__device__ __forceinline__ bf16x8 rowsum_selector(uint32_t lane) {
+    const __bf16 s = static_cast<__bf16>((((lane >> 4) ^ (lane >> 2)) & 1u) ? 0.0f : 1.0f);
+    return bf16x8{s, s, s, s, s, s, s, s};
+}
+
 template <int HD, int W>
 struct TileShape {
     static constexpr int KS = HD / 16;               // Q.K^T k-steps
@@ -499,7 +520,9 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     };
 
     float m_run = 0.0f;
-    float l_run = 0.0f;
+    float l_run = 0.0f;  // tile 0's f32 sum over the lane's keys, then the row sum
+    floatx4 l4 = {};     // the row sum after tile 0 (every lane holds its row's)
+    const bf16x8 sel = rowsum_selector(lane);
     floatx16 o_acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
@@ -590,7 +613,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
             if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazyLog2) != 0) {
                 const float m_new = fmaxf(m_run, mt);
                 const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                l_run *= alpha;
+                l4 *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
                 m_run = m_new;
@@ -613,12 +636,16 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
                     l_run += p;
                 }
             }
-            if constexpr (!first) l_run = sum8(pb_hi, l_run);
+            if constexpr (!first) l4 = mfma16x16x32(sel, pb_hi, l4);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 if constexpr (first) o_acc[dt] = mfma32x32x16(vf[j][dt], pb_lo, o_acc[dt]);
                 o_acc[dt] = mfma32x32x16(vf[j][dt], pb_hi, o_acc[dt]);
             }
+        }
+        if constexpr (first) {
+            const float l_row = l_run + __shfl_xor(l_run, 32, 64);
+            l4 = floatx4{l_row, l_row, l_row, l_row};
         }
         }
     staged:
@@ -645,6 +672,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         if (fixed || live) {
             m_run = 0.0f;
             l_run = 0.0f;
+            l4 = floatx4{};
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
         }
@@ -665,7 +693,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         // The DMA of the tiles past the end is still in flight: it must land
         // before the stages are refilled or the workgroup's LDS is released.
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-        if (fixed || live) l_run += __shfl_xor(l_run, 32, 64);
+        if (fixed || live) l_run = l4[0];
     };
 
     // Fixed softmax offset: m_run stays at the row's tile-0 max.  A later
@@ -747,6 +775,388 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Head_dim 128 with GQA 4 (the Llama-3-8B shape): the same work item (64
+// query rows x the 4 query heads of KV head k) served by 4 wavefronts, one
+// per query head and one per SIMD, each holding both 32-row groups.  Every
+// K or V fragment read from LDS then feeds two MFMAs (half the LDS reads per
+// MFMA of the 8-wavefront kernel), and the steady-state KV tiles run a
+// software pipeline written as one inline-asm loop (prefill_pipe_loop.inc,
+// generated by gen_prefill_pipe.py): iteration t issues the Q.K^T MFMAs of
+// tile t + 1 between the softmax instructions of tile t, then tile t's P.V.
+// On gfx950 VALU instructions co-issue with a running 32-cycle MFMA, so the
+// softmax no longer takes turns with the MFMAs.
+//
+// Four LDS stages (the tile in P.V, the tile in Q.K^T, and two in flight):
+// the DMA of tile t + 3 is issued at iteration t, after a barrier that
+// follows the wait for tile t + 1.  Tile 0 (whose max becomes the fixed
+// softmax offset and whose P goes in as bf16 hi + lo), the masked tiles at
+// the diagonal and the running-max recompute run as ordinary code.  Per row
+// the arithmetic is the 32-row kernels' operation for operation (same
+// MFMAs in the same order from the same LDS bytes, same VALU operations),
+// so a row gets the same bits here as in prefill_dma_kernel<128, 4, 1>,
+// which serves the same items on small grids.
+#include "prefill_pipe_loop.inc"
+
+// The four words of a raw buffer resource, for an inline-asm operand.
+__device__ __forceinline__ u32x4 rsrc_words(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xffffu, bytes,
+                 kBufferRsrcWord3};
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(
+        reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t *)p));
+}
+
+constexpr int kPipeStage = 32768;  // one stage: K (16 KiB) then V (16 KiB)
+constexpr int kPipeBT = 4096;      // one (block, KV head) tile at head_dim 128
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_pipe_kernel(
+    const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
+    const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
+    const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
+    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2, uint32_t fixed_offset,
+    uint32_t pool_bytes) {
+    constexpr int HD = 128, G = 4, KS = 8, DT = 4;
+    constexpr uint32_t kTile = kBS * HD;
+
+    // The table gets 16 entries of padding (copies of the last block id):
+    // the DMA runs up to three tiles past the last one, and the loop reads
+    // the ids of the tile after that, so no read needs a clamp.
+    __shared__ __align__(16) uint32_t tbl[kTableLds + 16];
+    __shared__ __align__(1024) uint8_t st[4 * kPipeStage];
+    __shared__ uint32_t redo;
+
+    const uint32_t kvh = blockIdx.x % kv_heads;
+    const uint32_t item = blockIdx.x / kv_heads;
+    const uint32_t row_begin = work[4 * item];
+    const uint32_t nrows = work[4 * item + 1];
+    const uint32_t p_min = work[4 * item + 2];
+    const uint32_t seq = work[4 * item + 3];
+    const uint32_t p_max = p_min + nrows - 1;
+    const uint32_t n_tiles = p_max / kKT + 1;
+    const uint32_t nblk = p_max / kBS + 1;  // <= kTableLds
+    const uint32_t *table = tables + table_off[seq];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t head = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t c = lane & 31;
+    const uint32_t gl = lane >> 5;
+    const uint32_t qhead = kvh * G + head;
+    bool row_ok[2];
+    uint32_t p_row[2], wp_min[2];
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+        row_ok[rg] = kRG * rg + c < nrows;
+        p_row[rg] = p_min + kRG * rg + c;
+        wp_min[rg] = p_min + kRG * rg;
+    }
+
+    {
+        const uint32_t ntbl = min(4 * n_tiles + 16, static_cast<uint32_t>(kTableLds + 16));
+        for (uint32_t i = tid; i < ntbl; i += 256) tbl[i] = table[min(i, nblk - 1)];
+    }
+    if (tid == 0) redo = 0u;
+
+    bf16x8 qv[2][KS];
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+        const uint16_t *qp =
+            q + (static_cast<uint64_t>(row_begin + kRG * rg + c) * num_heads + qhead) * HD + 8 * gl;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+            qv[rg][kk] = row_ok[rg] ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 16 * kk))
+                                    : bf16x8{};
+    }
+    wait_barrier<0>();  // the table copy
+
+    // DMA: the wave copies 1 KiB (part `head` of 4) of each of the tile's
+    // four blocks, K then V; lane L reads logical unit U of physical unit
+    // P = 64 head + L, as prefill_dma_kernel's stage layout has it.
+    const uint32_t dma_unit = 64 * head + lane;
+    const uint32_t dma_k = (dma_unit ^ ((dma_unit >> 4) & 3u)) * 16;
+    const uint32_t dma_v = (dma_unit ^ ((dma_unit >> 4) & 1u)) * 16;
+    const u32x4 krs = rsrc_words(k_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
+    const u32x4 vrs = rsrc_words(v_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
+    const uint32_t stride = kv_heads * kPipeBT;
+    const uint32_t st0 = lds_addr(st);
+    const uint32_t wbase = st0 + 1024 * head;
+    auto dma = [&](uint32_t t) __attribute__((always_inline)) {
+        uint32_t b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = uniform_u32(tbl[4 * t + i]) * stride;
+        const uint32_t w = uniform_u32(wbase + (t % 4) * kPipeStage);
+        asm volatile(
+            "s_mov_b32 m0, %[w]\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b0] offen lds\n"
+            "s_add_u32 m0, %[w], 4096\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b1] offen lds\n"
+            "s_add_u32 m0, %[w], 8192\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b2] offen lds\n"
+            "s_add_u32 m0, %[w], 12288\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b3] offen lds\n"
+            "s_add_u32 m0, %[w], 16384\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b0] offen lds\n"
+            "s_add_u32 m0, %[w], 20480\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b1] offen lds\n"
+            "s_add_u32 m0, %[w], 24576\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b2] offen lds\n"
+            "s_add_u32 m0, %[w], 28672\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b3] offen lds\n"
+            :
+            : [w] "s"(w), [krs] "s"(krs), [vrs] "s"(vrs), [dk] "v"(dma_k), [dv] "v"(dma_v),
+              [b0] "s"(b[0]), [b1] "s"(b[1]), [b2] "s"(b[2]), [b3] "s"(b[3])
+            : "m0", "scc", "memory");  // s_add_u32 writes scc
+    };
+
+    // LDS read offsets within a stage (prefill_dma_kernel's): K A-row c
+    // reads key key_perm(c); V A-row c reads dim 32 dt + c.
+    const uint32_t kp = key_perm(c);
+    const uint32_t kx = ((kp & 15) >> 2) & 3;
+    const uint32_t k_rd0 = (kp / 16) * kPipeBT + (kp & 15) * 64 + 16 * (gl ^ kx);
+    const uint32_t k_rd1 = (kp / 16) * kPipeBT + (kp & 15) * 64 + 16 * ((gl ^ kx) ^ 2);
+    const uint32_t v_rd = 4 * kPipeBT + c * 32 + 16 * (gl ^ ((c >> 3) & 1));
+
+    floatx16 o_acc[2][DT];
+    float m_run[2], l_run[2];
+    floatx4 l4[2] = {};  // row sums after tile 0 (prefill_dma_kernel's l4)
+    const bf16x8 sel = rowsum_selector(lane);
+
+    // One KV tile as ordinary code for both row groups: Q.K^T (unless the
+    // scores come in as s_in), the causal mask, the softmax (fixed offset,
+    // or the running max when `running`), P.V.  first: tile 0 (the offset
+    // is its max; P as bf16 hi + lo; the row sum adds the f32 P).
+    auto tile_step = [&](auto first_c, auto running_c, uint32_t t, const floatx16 (*s_in)[2],
+                         const bool (&live)[2]) __attribute__((always_inline)) {
+        constexpr bool first = decltype(first_c)::value;
+        constexpr bool running = decltype(running_c)::value;
+        const uint8_t *tile = st + (t % 4) * kPipeStage;
+        const uint32_t j0 = t * kKT;
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+            if (!live[rg]) continue;
+            floatx16 s0 = {}, s1 = {};
+            if (s_in != nullptr) {
+                s0 = s_in[rg][0];
+                s1 = s_in[rg][1];
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) {
+                    const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(tile + off);
+                    const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * kPipeBT);
+                    s0 = mfma32x32x16(ka, qv[rg][kk], s0);
+                    s1 = mfma32x32x16(kb, qv[rg][kk], s1);
+                }
+            }
+            float sc[32];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                sc[r] = s0[r];
+                sc[16 + r] = s1[r];
+            }
+            if (j0 + kKT - 1 > wp_min[rg]) {
+#pragma unroll
+                for (int r = 0; r < 32; ++r) {
+                    const uint32_t key = j0 + 32 * (r >> 4) + 16 * ((r >> 3) & 1) + 8 * gl + (r & 7);
+                    sc[r] = (key <= p_row[rg]) ? sc[r] : -INFINITY;
+                }
+            }
+            auto tile_max = [&]() __attribute__((always_inline)) {
+                float mx = sc[0];
+#pragma unroll
+                for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                return mx * scale_log2;
+            };
+            if constexpr (first) {
+                m_run[rg] = tile_max();
+            } else if constexpr (running) {
+                const float mt = tile_max();
+                if (__builtin_amdgcn_ballot_w64(mt > m_run[rg] + kLazyLog2) != 0) {
+                    const float m_new = fmaxf(m_run[rg], mt);
+                    const float alpha = __builtin_amdgcn_exp2f(m_run[rg] - m_new);
+                    l4[rg] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] *= alpha;
+                    m_run[rg] = m_new;
+                }
+            }
+            const float nm = -m_run[rg];
+#pragma unroll
+            for (int r = 0; r < 32; ++r) sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, nm));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                bf16x8 pb_hi, pb_lo;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float p = sc[16 * (j >> 1) + 8 * (j & 1) + i];
+                    const __bf16 hi = static_cast<__bf16>(p);
+                    pb_hi[i] = hi;
+                    if constexpr (first) {
+                        pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+                        l_run[rg] += p;
+                    }
+                }
+                if constexpr (!first) l4[rg] = mfma16x16x32(sel, pb_hi, l4[rg]);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const bf16x8 vf =
+                        *reinterpret_cast<const bf16x8 *>(tile + v_rd + j * kPipeBT + dt * 1024);
+                    if constexpr (first) o_acc[rg][dt] = mfma32x32x16(vf, pb_lo, o_acc[rg][dt]);
+                    o_acc[rg][dt] = mfma32x32x16(vf, pb_hi, o_acc[rg][dt]);
+                }
+            }
+            if constexpr (first) {
+                const float l_row = l_run[rg] + __shfl_xor(l_run[rg], 32, 64);
+                l4[rg] = floatx4{l_row, l_row, l_row, l_row};
+            }
+        }
+    };
+
+    using True = std::true_type;
+    using False = std::false_type;
+
+    // One pass as ordinary code, for the row groups in `live`: running max
+    // (the recompute) or the fixed offset (when the pipelined loop is off).
+    auto plain_pass = [&](auto running_c, const bool (&live)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+            if (!live[rg]) continue;
+            m_run[rg] = 0.0f;
+            l_run[rg] = 0.0f;
+            l4[rg] = floatx4{};
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
+        }
+        dma(0);
+        dma(1);
+        dma(2);
+        wait_barrier<16>();
+        dma(3);
+        tile_step(True{}, running_c, 0, nullptr, live);
+        for (uint32_t t = 1; t < n_tiles; ++t) {
+            wait_barrier<16>();
+            dma(t + 3);
+            tile_step(False{}, running_c, t, nullptr, live);
+        }
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the DMA past the end
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg)
+            if (live[rg]) l_run[rg] = l4[rg][0];
+    };
+
+    const bool both[2] = {true, true};
+    if (fixed_offset) {
+        // Tile 0 here, tiles 1 .. n - 1 in the pipelined loop.
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+            l_run[rg] = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
+        }
+        dma(0);
+        dma(1);
+        dma(2);
+        wait_barrier<16>();
+        dma(3);
+        tile_step(True{}, False{}, 0, nullptr, both);
+        if (n_tiles >= 2) {
+            // Tiles from `tmask` (a key index) on need the causal mask: the
+            // first is the one holding row group 0's first row's last
+            // visible key + 1.
+            const uint32_t tmask = kKT * ((p_min + 1) / kKT);
+            float nm0 = -m_run[0], nm1 = -m_run[1];
+            uint32_t vtbl = lds_addr(tbl) + 16 * 4;  // the ids of tile 4
+            const int32_t pr0 = static_cast<int32_t>(p_row[0] - 8 * gl);
+            const int32_t pr1 = static_cast<int32_t>(p_row[1] - 8 * gl);
+            uint32_t t_reg, j0_reg, b0, b1, b2, b3;
+            uint64_t mk0, mk1, mk2;
+            asm volatile(VO_PREFILL_PIPE_LOOP
+                         : "+{a[0:15]}"(o_acc[0][0]), "+{a[16:31]}"(o_acc[0][1]),
+                           "+{a[32:47]}"(o_acc[0][2]), "+{a[48:63]}"(o_acc[0][3]),
+                           "+{a[64:79]}"(o_acc[1][0]), "+{a[80:95]}"(o_acc[1][1]),
+                           "+{a[96:111]}"(o_acc[1][2]), "+{a[112:127]}"(o_acc[1][3]),
+                           "+{v[168:171]}"(l4[0]), "+{v[172:175]}"(l4[1]), "+{v189}"(vtbl),
+                           [t] "=&s"(t_reg), [j0] "=&s"(j0_reg), [b0] "=&s"(b0), [b1] "=&s"(b1),
+                           [b2] "=&s"(b2), [b3] "=&s"(b3), [m0] "=&s"(mk0), [m1] "=&s"(mk1),
+                           [m2] "=&s"(mk2)
+                         : "{a[128:131]}"(qv[0][0]), "{a[132:135]}"(qv[0][1]),
+                           "{a[136:139]}"(qv[0][2]), "{a[140:143]}"(qv[0][3]),
+                           "{a[144:147]}"(qv[0][4]), "{a[148:151]}"(qv[0][5]),
+                           "{a[152:155]}"(qv[0][6]), "{a[156:159]}"(qv[0][7]),
+                           "{a[160:163]}"(qv[1][0]), "{a[164:167]}"(qv[1][1]),
+                           "{a[168:171]}"(qv[1][2]), "{a[172:175]}"(qv[1][3]),
+                           "{a[176:179]}"(qv[1][4]), "{a[180:183]}"(qv[1][5]),
+                           "{a[184:187]}"(qv[1][6]), "{a[188:191]}"(qv[1][7]),
+                           "{v164}"(nm0), "{v165}"(nm1), "{v[176:179]}"(sel),
+                           "{v181}"(st0 + k_rd0), "{v182}"(st0 + k_rd1), "{v185}"(st0 + v_rd),
+                           "{v187}"(dma_k), "{v188}"(dma_v), "{v190}"(pr0), "{v191}"(pr1), [krs] "s"(krs),
+                           [vrs] "s"(vrs), [wbase] "s"(wbase), [stride] "s"(stride),
+                           [tend] "s"(n_tiles), [tmask] "s"(tmask), [scale] "s"(scale_log2)
+                         : VO_PREFILL_PIPE_CLOBBERS, "m0", "scc", "memory");
+        }
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+            l_run[rg] = l4[rg][0];
+            bool ok = l_run[rg] < kOverflowSum;  // false for inf and NaN too
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) ok = ok && __builtin_isfinite(o_acc[rg][dt][r]);
+            if (__builtin_amdgcn_ballot_w64(row_ok[rg] && !ok) != 0 && lane == 0)
+                atomicOr(&redo, 1u << rg);
+        }
+    } else if (tid == 0) {
+        redo = 3u;
+    }
+    wait_barrier<0>();
+    const uint32_t again = uniform_u32(redo);
+    if (again != 0) {
+        // The recompute with the running max for the 32-row groups that
+        // left the fixed-offset range (prefill_dma_kernel's second pass).
+        const bool live[2] = {(again & 1u) != 0, (again & 2u) != 0};
+        wait_barrier<0>();
+        plain_pass(True{}, live);
+    }
+    wait_barrier<0>();
+
+    // Output through LDS, as prefill_dma_kernel: the tile of (row group rg,
+    // head h) is tile 4 rg + h, 8 KiB each, chunk q of row c at q ^ (c % 16).
+    constexpr int ROWB = HD * 2;
+    constexpr int CH = HD / 8;
+    constexpr int WTILE = kRG * ROWB;
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+        const float inv = 1.0f / l_run[rg];
+        uint8_t *tile = st + (4 * rg + head) * WTILE + c * ROWB + 8 * gl;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                u32x2 packed;
+                packed[0] = f32_to_bf16_bits(o_acc[rg][dt][4 * r4] * inv) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[rg][dt][4 * r4 + 1] * inv)) << 16);
+                packed[1] = f32_to_bf16_bits(o_acc[rg][dt][4 * r4 + 2] * inv) |
+                            (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[rg][dt][4 * r4 + 3] * inv)) << 16);
+                const uint32_t q4 = static_cast<uint32_t>(4 * dt + r4) ^ (c % CH);
+                *reinterpret_cast<u32x2 *>(tile + 16 * q4) = packed;
+            }
+        }
+    }
+    wait_barrier<0>();
+    constexpr uint32_t kRowChunks = G * CH;
+    uint16_t *obase = out + (static_cast<uint64_t>(row_begin) * num_heads + kvh * G) * HD;
+    for (uint32_t k = tid; k < nrows * kRowChunks; k += 256) {
+        const uint32_t row = k / kRowChunks;
+        const uint32_t h = (k % kRowChunks) / CH;
+        const uint32_t q4 = k % CH;
+        const uint32_t w = h + G * (row / kRG);
+        const uint32_t cr = row % kRG;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(st + w * WTILE + cr * ROWB +
+                                                         16 * (q4 ^ (cr % CH)));
+        *reinterpret_cast<u32x4 *>(obase + static_cast<uint64_t>(row) * num_heads * HD + h * HD +
+                                   8 * q4) = v;
+    }
+}
+
 // VO_PREFILL_STAGING=regs selects the register-staged kernel above (A/B).
 bool prefill_use_dma() {
     static const bool dma = [] {
@@ -768,6 +1178,13 @@ bool prefill_fixed_offset() {
 // every launch.
 bool prefill_narrow_enabled() {
     const char *v = std::getenv("VO_PREFILL_NARROW");
+    return !(v && std::string(v) == "0");
+}
+
+// VO_PREFILL_PIPE=0 runs the 8-wavefront DMA kernel instead of the
+// pipelined one at head_dim 128, GQA 4 (A/B).  Read at every launch.
+bool prefill_pipe_enabled() {
+    const char *v = std::getenv("VO_PREFILL_PIPE");
     return !(v && std::string(v) == "0");
 }
 
@@ -799,6 +1216,18 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
                            dim3(64 * G * R), 0, stream, pool.k, pool.v, pool.kv_heads,
                            meta.table_off, meta.tables, plan.work, q, out, num_heads, scale_log2);
         if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
+    }
+    if constexpr (HD == 128 && G == 4 && R == 2) {
+        // 64-row workgroups at the Llama-3-8B shape: the pipelined kernel.
+        if (regs_items < plan.num_items && prefill_pipe_enabled()) {
+            KernelTimer timer("prefill_pipe", stream);
+            hipLaunchKernelGGL(prefill_pipe_kernel, dim3((plan.num_items - regs_items) * per_item),
+                               dim3(256), 0, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
+                               meta.tables, plan.work + 4 * static_cast<uint64_t>(regs_items), q,
+                               out, num_heads, scale_log2, prefill_fixed_offset() ? 1u : 0u,
+                               static_cast<uint32_t>(pool.elems * 2));
+            return hipGetLastError();
+        }
     }
     if constexpr (dma_shape) {
         if (regs_items < plan.num_items) {
