@@ -124,6 +124,20 @@ __device__ __forceinline__ bf16x8 rowsum_selector(uint32_t lane) {
     return bf16x8{s, s, s, s, s, s, s, s};
 }
 
+// True when every element of the DT accumulator blocks is finite: fma(x, 0,
+// acc) keeps acc at exactly +0 for finite x and turns it into NaN for an
+// infinite or NaN x.  (One VALU op per element; a chain of v_cmp_class
+// lane masks ANDed on the scalar unit waits on every VALU result.)
+template <int DT>
+__device__ __forceinline__ bool all_finite(const floatx16 (&o)[DT]) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r & 3] = __builtin_fmaf(o[dt][r], 0.0f, acc[r & 3]);
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]) == 0.0f;
+}
+
 template <int HD, int W>
 struct TileShape {
     static constexpr int KS = HD / 16;               // Q.K^T k-steps
@@ -711,11 +725,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     // items avoids): the same rows give the same bits in any batch.
     if (fixed_offset) {
         pass(std::true_type{});
-        bool ok = l_run < kOverflowSum;  // false for inf and NaN too
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) ok = ok && __builtin_isfinite(o_acc[dt][r]);
+        const bool ok = l_run < kOverflowSum && all_finite(o_acc);  // false for inf and NaN too
         if (__builtin_amdgcn_ballot_w64(row_ok && !ok) != 0 && lane == 0) atomicOr(&redo, 1u << rg);
     } else if (tid == 0) {
         redo = (1u << R) - 1;
@@ -856,6 +866,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         wp_min[rg] = p_min + kRG * rg;
     }
 
+
+    // DMA: the wave copies 1 KiB (part `head` of 4) of each of the tile's
+    // four blocks, K then V; lane L reads logical unit U of physical unit
+    // P = 64 head + L, as prefill_dma_kernel's stage layout has it.
+    const uint32_t dma_unit = 64 * head + lane;
+    const uint32_t dma_k = (dma_unit ^ ((dma_unit >> 4) & 3u)) * 16;
+    const uint32_t dma_v = (dma_unit ^ ((dma_unit >> 4) & 1u)) * 16;
+    const u32x4 krs = rsrc_words(k_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
+    const u32x4 vrs = rsrc_words(v_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
+    const uint32_t stride = kv_heads * kPipeBT;
+    const uint32_t st0 = lds_addr(st);
+    const uint32_t wbase = st0 + 1024 * head;
+    // LDS DMA of tile t with block byte offsets b into its stage.
+    auto dma_raw = [&](uint32_t t, const uint32_t (&b)[4]) __attribute__((always_inline)) {
+        const uint32_t w = uniform_u32(wbase + (t % 4) * kPipeStage);
+        asm volatile(
+            "s_mov_b32 m0, %[w]\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b0] offen lds\n"
+            "s_add_u32 m0, %[w], 4096\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b1] offen lds\n"
+            "s_add_u32 m0, %[w], 8192\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b2] offen lds\n"
+            "s_add_u32 m0, %[w], 12288\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b3] offen lds\n"
+            "s_add_u32 m0, %[w], 16384\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b0] offen lds\n"
+            "s_add_u32 m0, %[w], 20480\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b1] offen lds\n"
+            "s_add_u32 m0, %[w], 24576\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b2] offen lds\n"
+            "s_add_u32 m0, %[w], 28672\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b3] offen lds\n"
+            :
+            : [w] "s"(w), [krs] "s"(krs), [vrs] "s"(vrs), [dk] "v"(dma_k), [dv] "v"(dma_v),
+              [b0] "s"(b[0]), [b1] "s"(b[1]), [b2] "s"(b[2]), [b3] "s"(b[3])
+            : "m0", "scc", "memory");  // s_add_u32 writes scc
+    };
+    // Tile t's block ids from the LDS table (padded: no clamp needed).
+    auto dma = [&](uint32_t t) __attribute__((always_inline)) {
+        uint32_t b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = uniform_u32(tbl[4 * t + i]) * stride;
+        dma_raw(t, b);
+    };
+    // The same with the ids read from the sequence's table in global memory
+    // (scalar loads, clamped to its last block), before the LDS copy exists.
+    auto dma_global = [&](uint32_t t) __attribute__((always_inline)) {
+        uint32_t b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b[i] = uniform_u32(table[min(4 * t + i, nblk - 1)]) * stride;
+        dma_raw(t, b);
+    };
+
+    // The first three tiles' DMA goes out first, so that its latency, the
+    // table copy's and Q's overlap behind one wait.
+    if (fixed_offset) {
+        dma_global(0);
+        dma_global(1);
+        dma_global(2);
+    }
     {
         const uint32_t ntbl = min(4 * n_tiles + 16, static_cast<uint32_t>(kTableLds + 16));
         for (uint32_t i = tid; i < ntbl; i += 256) tbl[i] = table[min(i, nblk - 1)];
@@ -872,38 +934,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             qv[rg][kk] = row_ok[rg] ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 16 * kk))
                                     : bf16x8{};
     }
-    wait_barrier<0>();  // the table copy
+    wait_barrier<0>();  // the table copy, Q and (fixed offset) tiles 0-2
 
-    // DMA: the wave copies 1 KiB (part `head` of 4) of each of the tile's
-    // four blocks, K then V; lane L reads logical unit U of physical unit
-    // P = 64 head + L, as prefill_dma_kernel's stage layout has it.
-    const uint32_t dma_unit = 64 * head + lane;
-    const uint32_t dma_k = (dma_unit ^ ((dma_unit >> 4) & 3u)) * 16;
-    const uint32_t dma_v = (dma_unit ^ ((dma_unit >> 4) & 1u)) * 16;
-    const u32x4 krs = rsrc_words(k_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
-    const u32x4 vrs = rsrc_words(v_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
-    const uint32_t stride = kv_heads * kPipeBT;
-    const uint32_t st0 = lds_addr(st);
-    const uint32_t wbase = st0 + 1024 * head;
-    auto dma = [&](uint32_t t) __attribute__((always_inline)) {
-        uint32_t b[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) b[i] = uniform_u32(tbl[4 * t + i]) * stride;
-        const uint32_t w = uniform_u32(wbase + (t % 4) * kPipeStage);
-        asm volatile(
-            "s_mov_b32 m0, %[w]\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b0] offen lds\n"
-            "s_add_u32 m0, %[w], 4096\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b1] offen lds\n"
-            "s_add_u32 m0, %[w], 8192\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b2] offen lds\n"
-            "s_add_u32 m0, %[w], 12288\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b3] offen lds\n"
-            "s_add_u32 m0, %[w], 16384\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b0] offen lds\n"
-            "s_add_u32 m0, %[w], 20480\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b1] offen lds\n"
-            "s_add_u32 m0, %[w], 24576\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b2] offen lds\n"
-            "s_add_u32 m0, %[w], 28672\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b3] offen lds\n"
-            :
-            : [w] "s"(w), [krs] "s"(krs), [vrs] "s"(vrs), [dk] "v"(dma_k), [dv] "v"(dma_v),
-              [b0] "s"(b[0]), [b1] "s"(b[1]), [b2] "s"(b[2]), [b3] "s"(b[3])
-            : "m0", "scc", "memory");  // s_add_u32 writes scc
-    };
 
     // LDS read offsets within a stage (prefill_dma_kernel's): K A-row c
     // reads key key_perm(c); V A-row c reads dim 32 dt + c.
@@ -1051,10 +1083,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
         }
-        dma(0);
-        dma(1);
-        dma(2);
-        wait_barrier<16>();
         dma(3);
         tile_step(True{}, False{}, 0, nullptr, both);
         if (n_tiles >= 2) {
@@ -1096,11 +1124,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg) {
             l_run[rg] = l4[rg][0];
-            bool ok = l_run[rg] < kOverflowSum;  // false for inf and NaN too
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) ok = ok && __builtin_isfinite(o_acc[rg][dt][r]);
+            const bool ok = l_run[rg] < kOverflowSum && all_finite(o_acc[rg]);  // false for inf, NaN
             if (__builtin_amdgcn_ballot_w64(row_ok[rg] && !ok) != 0 && lane == 0)
                 atomicOr(&redo, 1u << rg);
         }

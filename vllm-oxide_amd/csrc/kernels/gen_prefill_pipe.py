@@ -217,10 +217,14 @@ class Body:
             self.lds_done = seq
 
 
-# Issue cost (cycles) of VALU ops when co-issued with MFMAs, and the VALU
-# budget of one 32-cycle MFMA slot.
+# Issue cost (cycles) of VALU ops, and the VALU budget of one 32-cycle MFMA
+# slot.  Spreading the softmax evenly over the MFMAs (about 14 cycles of
+# VALU per slot here) runs a tile in ~2,355 cycles against ~2,515 when each
+# slot is filled to 28 cycles first (probe of this loop with static LDS,
+# MFMA floor 2,176): co-issued VALU still costs about a cycle per op, more
+# when bunched.
 COST = {"v_exp_f32": 9, "s_nop": 2}
-BUDGET = 28
+BUDGET = 16
 
 
 def cost(op):
