@@ -103,27 +103,6 @@ __device__ __forceinline__ float sum8(bf16x8 v, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), one, acc, false);
 }
 
-__device__ __forceinline__ floatx4 mfma16x16x32(bf16x8 a, bf16x8 b, floatx4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Row sums on the matrix core.  The P operand of the P.V MFMA (32 rows x 16
-// keys: lane l holds 8 keys of row l % 32) fed as the B operand of
-// v_mfma_f32_16x16x32_bf16 makes lane l's 8 values the 32-deep column
-// l % 16's k-slice of lane group g = l / 16.  With every value of A-lane
-// a = 16 g + m set to 1 when g and m / 4 have the same parity (else 0),
-// output element (m, n) adds the 8-value slices of B-lanes n + 16 g over
-// the groups g with g % 2 == (m / 4) % 2: both key halves of row
-// n + 16 ((m / 4) % 2).  Output lane l holds rows m = 4 (l / 16) + r of
-// column l % 16, so all four of its values are the sum of its own row
-// l % 32.  Eight v_dot2c per 16 keys would block the MFMA pipe (a dot
-// instruction does not co-issue with MFMAs on gfx950); this takes one
-// 16-cycle MFMA.
-__device__ __forceinline__ bf16x8 rowsum_selector(uint32_t lane) {
-    const __bf16 s = static_cast<__bf16>((((lane >> 4) ^ (lane >> 2)) & 1u) ? 0.0f : 1.0f);
-    return bf16x8{s, s, s, s, s, s, s, s};
-}
-
 // True when every element of the DT accumulator blocks is finite: fma(x, 0,
 // acc) keeps acc at exactly +0 for finite x and turns it into NaN for an
 // infinite or NaN x.  (One VALU op per element; a chain of v_cmp_class
@@ -534,9 +513,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
     };
 
     float m_run = 0.0f;
-    float l_run = 0.0f;  // tile 0's f32 sum over the lane's keys, then the row sum
-    floatx4 l4 = {};     // the row sum after tile 0 (every lane holds its row's)
-    const bf16x8 sel = rowsum_selector(lane);
+    float l_run = 0.0f;  // the f32 sum of the lane's p, then (after the pass) the row's
     floatx16 o_acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
@@ -627,7 +604,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
             if (__builtin_amdgcn_ballot_w64(mt > m_run + kLazyLog2) != 0) {
                 const float m_new = fmaxf(m_run, mt);
                 const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                l4 *= alpha;
+                l_run *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) o_acc[dt] *= alpha;
                 m_run = m_new;
@@ -645,21 +622,14 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
                 const float p = sc[16 * (j >> 1) + 8 * (j & 1) + i];
                 const __bf16 hi = static_cast<__bf16>(p);
                 pb_hi[i] = hi;
-                if constexpr (first) {
-                    pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
-                    l_run += p;
-                }
+                if constexpr (first) pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+                l_run += p;
             }
-            if constexpr (!first) l4 = mfma16x16x32(sel, pb_hi, l4);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 if constexpr (first) o_acc[dt] = mfma32x32x16(vf[j][dt], pb_lo, o_acc[dt]);
                 o_acc[dt] = mfma32x32x16(vf[j][dt], pb_hi, o_acc[dt]);
             }
-        }
-        if constexpr (first) {
-            const float l_row = l_run + __shfl_xor(l_run, 32, 64);
-            l4 = floatx4{l_row, l_row, l_row, l_row};
         }
         }
     staged:
@@ -686,7 +656,6 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         if (fixed || live) {
             m_run = 0.0f;
             l_run = 0.0f;
-            l4 = floatx4{};
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o_acc[dt] = floatx16{};
         }
@@ -707,7 +676,7 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
         // The DMA of the tiles past the end is still in flight: it must land
         // before the stages are refilled or the workgroup's LDS is released.
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-        if (fixed || live) l_run = l4[0];
+        if (fixed || live) l_run += __shfl_xor(l_run, 32, 64);
     };
 
     // Fixed softmax offset: m_run stays at the row's tile-0 max.  A later
@@ -947,8 +916,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     floatx16 o_acc[2][DT];
     float m_run[2], l_run[2];
-    floatx4 l4[2] = {};  // row sums after tile 0 (prefill_dma_kernel's l4)
-    const bf16x8 sel = rowsum_selector(lane);
 
     // One KV tile as ordinary code for both row groups: Q.K^T (unless the
     // scores come in as s_in), the causal mask, the softmax (fixed offset,
@@ -1004,7 +971,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 if (__builtin_amdgcn_ballot_w64(mt > m_run[rg] + kLazyLog2) != 0) {
                     const float m_new = fmaxf(m_run[rg], mt);
                     const float alpha = __builtin_amdgcn_exp2f(m_run[rg] - m_new);
-                    l4[rg] *= alpha;
+                    l_run[rg] *= alpha;
 #pragma unroll
                     for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] *= alpha;
                     m_run[rg] = m_new;
@@ -1021,12 +988,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     const float p = sc[16 * (j >> 1) + 8 * (j & 1) + i];
                     const __bf16 hi = static_cast<__bf16>(p);
                     pb_hi[i] = hi;
-                    if constexpr (first) {
-                        pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
-                        l_run[rg] += p;
-                    }
+                    if constexpr (first) pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
+                    l_run[rg] += p;
                 }
-                if constexpr (!first) l4[rg] = mfma16x16x32(sel, pb_hi, l4[rg]);
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
                     const bf16x8 vf =
@@ -1034,10 +998,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     if constexpr (first) o_acc[rg][dt] = mfma32x32x16(vf, pb_lo, o_acc[rg][dt]);
                     o_acc[rg][dt] = mfma32x32x16(vf, pb_hi, o_acc[rg][dt]);
                 }
-            }
-            if constexpr (first) {
-                const float l_row = l_run[rg] + __shfl_xor(l_run[rg], 32, 64);
-                l4[rg] = floatx4{l_row, l_row, l_row, l_row};
             }
         }
     };
@@ -1053,7 +1013,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             if (!live[rg]) continue;
             m_run[rg] = 0.0f;
             l_run[rg] = 0.0f;
-            l4[rg] = floatx4{};
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
         }
@@ -1071,7 +1030,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the DMA past the end
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg)
-            if (live[rg]) l_run[rg] = l4[rg][0];
+            if (live[rg]) l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
     };
 
     const bool both[2] = {true, true};
@@ -1101,7 +1060,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                            "+{a[32:47]}"(o_acc[0][2]), "+{a[48:63]}"(o_acc[0][3]),
                            "+{a[64:79]}"(o_acc[1][0]), "+{a[80:95]}"(o_acc[1][1]),
                            "+{a[96:111]}"(o_acc[1][2]), "+{a[112:127]}"(o_acc[1][3]),
-                           "+{v[168:171]}"(l4[0]), "+{v[172:175]}"(l4[1]), "+{v189}"(vtbl),
+                           "+{v166}"(l_run[0]), "+{v167}"(l_run[1]), "+{v189}"(vtbl),
                            [t] "=&s"(t_reg), [j0] "=&s"(j0_reg), [b0] "=&s"(b0), [b1] "=&s"(b1),
                            [b2] "=&s"(b2), [b3] "=&s"(b3), [m0] "=&s"(mk0), [m1] "=&s"(mk1),
                            [m2] "=&s"(mk2)
@@ -1113,7 +1072,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                            "{a[168:171]}"(qv[1][2]), "{a[172:175]}"(qv[1][3]),
                            "{a[176:179]}"(qv[1][4]), "{a[180:183]}"(qv[1][5]),
                            "{a[184:187]}"(qv[1][6]), "{a[188:191]}"(qv[1][7]),
-                           "{v164}"(nm0), "{v165}"(nm1), "{v[176:179]}"(sel),
+                           "{v164}"(nm0), "{v165}"(nm1),
                            "{v181}"(st0 + k_rd0), "{v182}"(st0 + k_rd1), "{v185}"(st0 + v_rd),
                            "{v187}"(dma_k), "{v188}"(dma_v), "{v190}"(pr0), "{v191}"(pr1), [krs] "s"(krs),
                            [vrs] "s"(vrs), [wbase] "s"(wbase), [stride] "s"(stride),
@@ -1123,7 +1082,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg) {
-            l_run[rg] = l4[rg][0];
+            l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
             const bool ok = l_run[rg] < kOverflowSum && all_finite(o_acc[rg]);  // false for inf, NaN
             if (__builtin_amdgcn_ballot_w64(row_ok[rg] && !ok) != 0 && lane == 0)
                 atomicOr(&redo, 1u << rg);

@@ -15,10 +15,9 @@ its first 16 keys.  Iteration t then issues, in MFMA order,
 
 and between them the VALU work: the softmax of tile t's keys 16-63 in P1
 and P2; in P3 the causal mask of tile t + 1 when it needs one and the
-softmax of its keys 0-15.  After each 16-key P.V block, one
-v_mfma_f32_16x16x32_bf16 per row group adds the block's P into the row
-sums (a 0/1 selector as A: every lane gets its own row's sum; v_dot2 would
-block the MFMA pipe).  On gfx950 independent VALU
+softmax of its keys 0-15.  The row sums add each f32 probability in key
+order (one v_add_f32 chain per lane and row group; a v_dot2 would block the
+MFMA pipe).  On gfx950 independent VALU
 instructions co-issue with a running 32-cycle v_mfma_f32_32x32x16_bf16, so
 the softmax runs under the MFMAs.  Iteration t starts with the wait for tile
 t + 1's DMA and a barrier (after which stage (t+3) % 4 is free: every wave
@@ -29,8 +28,8 @@ Each K or V fragment read from LDS feeds two MFMAs (the two row groups).
 Per row the arithmetic is the 32-row kernels' operation for operation: S
 accumulates the eight 16-dim k-steps in order from zero, masked scores are
 -inf, p = exp2(fma(s, scale, -m)), P is rounded to bf16 (nearest even), the
-row sum adds each 16-key block of bf16 P with the selector MFMA, and O
-accumulates a tile's four 16-key steps in order.
+row sum adds the f32 p in key order (each lane its 32 keys of the tile),
+and O accumulates a tile's four 16-key steps in order.
 
 Register map (physical; the kernel pins its operands to these):
     a[0:127]    O: block (rg, dt) at a[16 (4 rg + dt)] (32 dims x 32 rows)
@@ -39,9 +38,7 @@ Register map (physical; the kernel pins its operands to these):
     v[0:63]     S buffer 0, v[64:127] S buffer 1; block (rg, h) at +16 (2 h + rg)
     v[128:159]  P: (rg, j) at v[128 + 16 rg + 4 j] (bf16 pairs)
     v[160:163]  block ids of the tile whose DMA the next iteration issues
-    v164, v165  -m (rg 0, 1)
-    v[168:171], v[172:175]  row sums (rg 0, 1; four copies per lane)
-    v[176:179]  the row-sum selector (A operand of v_mfma_f32_16x16x32_bf16)
+    v164, v165  -m (rg 0, 1)           v166, v167  row sums (rg 0, 1; per lane)
     v180        -inf
     v181, v182  K read address at stage 0 (even / odd k-steps); v183, v184 + 64 KiB
     v185        V read address at stage 0; v186 + 64 KiB
@@ -127,8 +124,8 @@ def pv_mfma(n, rg):
 
 
 def softmax_j(buf, j):
-    """fma + exp + bf16 pack of the 16 scores (8 per row group) of 16-key
-    step j of the S buffer into P(rg, j).  The two row groups' chains are
+    """fma + exp + row-sum add + bf16 pack of the 16 scores (8 per row
+    group) of 16-key step j of the S buffer into P(rg, j).  The two row groups' chains are
     interleaved and each exp trails its fma by two ops, so exps (the
     slow VALU op) spread out; a pack follows its second exp by at least
     two ops (a transcendental result needs one wait state)."""
@@ -138,6 +135,7 @@ def softmax_j(buf, j):
     ex = [f"v_exp_f32 v{base[rg] + i}, v{base[rg] + i}" for i in range(8) for rg in range(2)]
     pk = {(rg, i): f"v_cvt_pk_bf16_f32 v{P(rg, j) + i // 2}, v{base[rg] + i}, v{base[rg] + i + 1}"
           for rg in range(2) for i in range(0, 8, 2)}
+    ad = [f"v_add_f32 v{166 + rg}, v{166 + rg}, v{base[rg] + i}" for i in range(8) for rg in range(2)]
     ops = fm[:4]
     pend = []  # (ops to wait, pack)
 
@@ -155,17 +153,12 @@ def softmax_j(buf, j):
             push(fm[k + 4])
         push(ex[k])
         i, rg = k // 2, k % 2
+        pend.append([2, ad[k]])
         if i % 2 == 1:
             pend.append([2, pk[(rg, i - 1)]])
     while pend:
         ops.append(pend.pop(0)[1])
     return ops
-
-
-def rowsum_mfma(rg, j):
-    """Adds the 16 keys of P(rg, j) into rg's row sums."""
-    L = 168 + 4 * rg
-    return f"v_mfma_f32_16x16x32_bf16 v[{L}:{L + 3}], v[176:179], v[{P(rg, j)}:{P(rg, j) + 3}], v[{L}:{L + 3}]"
 
 
 def mask_ops(buf):
@@ -330,8 +323,6 @@ def iteration(stage, masked_next, last):
                 if key:
                     first_use.setdefault(key, len(mfmas))
                 mfmas.append((pv_mfma(nv, rg), key, [P(rg, j)]))
-        for rg in range(2):
-            mfmas.append((rowsum_mfma(rg, j), None, [P(rg, j)]))
 
     pv_block(0)
     if not last:
