@@ -917,12 +917,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     floatx16 o_acc[2][DT];
     float m_run[2], l_run[2];
 
-    // One KV tile as ordinary code for both row groups: Q.K^T (unless the
-    // scores come in as s_in), the causal mask, the softmax (fixed offset,
+    // One KV tile as ordinary code for both row groups: Q.K^T, the causal mask, the softmax (fixed offset,
     // or the running max when `running`), P.V.  first: tile 0 (the offset
     // is its max; P as bf16 hi + lo; the row sum adds the f32 P).
-    auto tile_step = [&](auto first_c, auto running_c, uint32_t t, const floatx16 (*s_in)[2],
-                         const bool (&live)[2]) __attribute__((always_inline)) {
+    auto tile_step = [&](auto first_c, auto running_c, uint32_t t, const bool (&live)[2])
+                         __attribute__((always_inline)) {
         constexpr bool first = decltype(first_c)::value;
         constexpr bool running = decltype(running_c)::value;
         const uint8_t *tile = st + (t % 4) * kPipeStage;
@@ -931,18 +930,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int rg = 0; rg < 2; ++rg) {
             if (!live[rg]) continue;
             floatx16 s0 = {}, s1 = {};
-            if (s_in != nullptr) {
-                s0 = s_in[rg][0];
-                s1 = s_in[rg][1];
-            } else {
 #pragma unroll
-                for (int kk = 0; kk < KS; ++kk) {
-                    const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
-                    const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(tile + off);
-                    const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * kPipeBT);
-                    s0 = mfma32x32x16(ka, qv[rg][kk], s0);
-                    s1 = mfma32x32x16(kb, qv[rg][kk], s1);
-                }
+            for (int kk = 0; kk < KS; ++kk) {
+                const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
+                const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(tile + off);
+                const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * kPipeBT);
+                s0 = mfma32x32x16(ka, qv[rg][kk], s0);
+                s1 = mfma32x32x16(kb, qv[rg][kk], s1);
             }
             float sc[32];
 #pragma unroll
@@ -1021,11 +1015,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         dma(2);
         wait_barrier<16>();
         dma(3);
-        tile_step(True{}, running_c, 0, nullptr, live);
+        tile_step(True{}, running_c, 0, live);
         for (uint32_t t = 1; t < n_tiles; ++t) {
             wait_barrier<16>();
             dma(t + 3);
-            tile_step(False{}, running_c, t, nullptr, live);
+            tile_step(False{}, running_c, t, live);
         }
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the DMA past the end
 #pragma unroll
@@ -1043,7 +1037,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
         }
         dma(3);
-        tile_step(True{}, False{}, 0, nullptr, both);
+        tile_step(True{}, False{}, 0, both);
         if (n_tiles >= 2) {
             // Tiles from `tmask` (a key index) on need the causal mask: the
             // first is the one holding row group 0's first row's last
