@@ -49,8 +49,10 @@ def _out(wl, backend):
 def _out_with_prefill_instances(vo, wl, backend):
     """_out with per-launch timing on; also the set of prefill kernel
     instances that ran (the library times each launch under its instance's
-    name: prefill_dma = 64-row workgroups, prefill_dma_narrow = 32-row
-    workgroups, prefill_regs = the register-staged kernel)."""
+    name: prefill_pipe = the pipelined 4-wavefront kernel for 64-row
+    workgroups at head_dim 128 / GQA 4, prefill_dma = the 8-wavefront kernel
+    for other 64-row workgroups, prefill_dma_narrow = 32-row workgroups,
+    prefill_regs = the register-staged kernel)."""
     import torch
     vo.profile_reset()
     vo.enable_profiling(True)
