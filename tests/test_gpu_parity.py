@@ -600,9 +600,10 @@ def test_prefill_64_row_workgroups_edge_shapes(vo, gpu_backend, monkeypatch, off
     _assert_close(out.float().cpu().numpy(), want, f"prefill 64-row workgroups ({offset})")
 
 
-@pytest.mark.parametrize("narrow,pipe", [("1", "1"), ("0", "1"), ("0", "0")])
+@pytest.mark.parametrize("narrow,pipe,slots", [("1", "1", ""), ("0", "1", ""), ("0", "1", "1"),
+                                               ("0", "0", "")])
 @pytest.mark.parametrize("factor", [4.0, 10.0])
-def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, pipe, factor):
+def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, pipe, slots, factor):
     """The prefill kernel first keeps each row's tile-0 max as its softmax
     offset.  Key 200 of sequence 0 (cached, KV tile 3) is set to factor x
     query row 0's head-0 vector (KV head 0 serves heads 0..3), so that row's
@@ -611,11 +612,15 @@ def test_prefill_key_far_above_tile0_max(vo, gpu_backend, monkeypatch, narrow, p
     factor 10, where 2^163 overflows f32 and only the recompute with the
     running max gives finite output.  Every row must match the oracle, in
     32-row (narrow) and 64-row workgroups (the pipelined kernel and the
-    8-wavefront one)."""
+    8-wavefront one).  slots "1": the pipelined kernel's five items run back
+    to back in one workgroup per KV head, the recomputed one third, between
+    items whose tiles it prefetched and that prefetched its own."""
     import torch
-    _say(f"prefill key far above tile-0 max (factor {factor}, narrow {narrow}, pipe {pipe})")
+    _say(f"prefill key far above tile-0 max (factor {factor}, narrow {narrow}, pipe {pipe}, "
+         f"slots {slots or 'default'})")
     monkeypatch.setenv("VO_PREFILL_NARROW", narrow)
     monkeypatch.setenv("VO_PREFILL_PIPE", pipe)
+    monkeypatch.setenv("VO_PREFILL_PIPE_SLOTS", slots)
     ctx, new = [300, 0, 900], [64, 128, 100]
     wl = W.build(vo, gpu_backend, kind="prefill", heads=32, kv_heads=8, head_dim=128,
                  block_size=16, num_blocks=200, context_lens=ctx, num_new=new, seed=62)
@@ -828,16 +833,21 @@ def test_prefill_cfg3_full_size_sampled_rows(vo, gpu_backend):
     _assert_close(out[rows], want, "cfg3")
 
 
-@pytest.mark.parametrize("case", ["cfg3", "edges"])
-def test_prefill_pipe_kernel_bitwise_equals_dma_kernel(vo, gpu_backend, monkeypatch, case):
+@pytest.mark.parametrize("case,slots", [("cfg3", ""), ("cfg3", "1"), ("edges", ""), ("edges", "1"),
+                                        ("edges", "3")])
+def test_prefill_pipe_kernel_bitwise_equals_dma_kernel(vo, gpu_backend, monkeypatch, case, slots):
     """The pipelined 4-wavefront kernel computes each row with the 32-row
     kernels' operations in their order, so its output is bitwise the
     8-wavefront DMA kernel's (VO_PREFILL_PIPE=0): at BASELINE config 3's full
     size, and on items that end before, at and past tile and 32-row-group
     boundaries (so that the pipelined loop runs 0, 1, 2 and many tiles and
-    the masked tiles follow it in either S buffer)."""
-    _say(f"prefill pipelined kernel vs DMA kernel bitwise ({case})")
+    the masked tiles follow it in either S buffer).  The kernel is
+    persistent: slots "1" and "3" deal all items to one or three workgroups
+    per KV head, so that items of every length follow each other through
+    the LDS ring (tile 0 at every stage, prefetched or not)."""
+    _say(f"prefill pipelined kernel vs DMA kernel bitwise ({case}, slots {slots or 'default'})")
     monkeypatch.setenv("VO_PREFILL_NARROW", "0")
+    monkeypatch.setenv("VO_PREFILL_PIPE_SLOTS", slots)
     if case == "cfg3":
         ctx, new = W.cfg3_context_lens(), [512] * 8
         nb = 12000

@@ -793,63 +793,108 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 constexpr int kPipeStage = 32768;  // one stage: K (16 KiB) then V (16 KiB)
 constexpr int kPipeBT = 4096;      // one (block, KV head) tile at head_dim 128
 
+// One work item of prefill_pipe_kernel, from its descriptor (first row, rows,
+// position of the first row, offset of the sequence's block table).
+struct PipeItem {
+    uint32_t row_begin, nrows, p_min, n_tiles, nblk;
+    const uint32_t *table;
+};
+
+__device__ __forceinline__ PipeItem pipe_item(const uint32_t *desc, const uint32_t *tables) {
+    PipeItem it;
+    it.row_begin = desc[0];
+    it.nrows = desc[1];
+    it.p_min = desc[2];
+    it.table = tables + desc[3];
+    const uint32_t p_max = it.p_min + it.nrows - 1;
+    it.n_tiles = p_max / kKT + 1;
+    it.nblk = p_max / kBS + 1;  // <= kTableLds
+    return it;
+}
+
+// Persistent: workgroup w serves KV head w % kv_heads and runs the items of
+// slot w / kv_heads (plan[slot] .. plan[slot + 1] - 1 of the descriptors at
+// plan + num_slots + 1) back to back.  The four LDS stages form one ring
+// across the items: item k's tile t sits in stage (T_k + t) % 4 with
+// T_k+1 = T_k + n_k, and the block table in LDS continues past an item's
+// last tile with the next item's first twelve block ids, so the DMAs the
+// loop issues past the end (tiles n .. n + 2) fetch the next item's tiles
+// 0-2 while this one finishes.  Its Q and block table load while this
+// item's output is written.  Each wave writes its own head's rows through
+// the one stage that holds no prefetched tile.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void prefill_pipe_kernel(
     const uint16_t *__restrict__ k_pool, const uint16_t *__restrict__ v_pool, uint32_t kv_heads,
-    const uint32_t *__restrict__ table_off, const uint32_t *__restrict__ tables,
-    const uint32_t *__restrict__ work, const uint16_t *__restrict__ q,
-    uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2, uint32_t fixed_offset,
-    uint32_t pool_bytes) {
+    const uint32_t *__restrict__ tables, const uint32_t *__restrict__ plan, uint32_t num_slots,
+    const uint16_t *__restrict__ q, uint16_t *__restrict__ out, uint32_t num_heads, float scale_log2,
+    uint32_t fixed_offset, uint32_t pool_bytes) {
     constexpr int HD = 128, G = 4, KS = 8, DT = 4;
     constexpr uint32_t kTile = kBS * HD;
 
-    // The table gets 16 entries of padding (copies of the last block id):
-    // the DMA runs up to three tiles past the last one, and the loop reads
-    // the ids of the tile after that, so no read needs a clamp.
+    // The table gets 16 entries past an item's last tile: the next item's
+    // first twelve block ids (or copies of the last one), since the DMA runs
+    // up to three tiles past the last one and the loop reads the ids of the
+    // tile after that.
     __shared__ __align__(16) uint32_t tbl[kTableLds + 16];
     __shared__ __align__(1024) uint8_t st[4 * kPipeStage];
-    __shared__ uint32_t redo;
+    // Overflow flags, alternating between consecutive items: item k sets
+    // redo[k % 2]; redo[(k + 1) % 2] is cleared after item k's first
+    // barrier, when every wave has read it for item k - 1.
+    __shared__ uint32_t redo[2];
 
     const uint32_t kvh = blockIdx.x % kv_heads;
-    const uint32_t item = blockIdx.x / kv_heads;
-    const uint32_t row_begin = work[4 * item];
-    const uint32_t nrows = work[4 * item + 1];
-    const uint32_t p_min = work[4 * item + 2];
-    const uint32_t seq = work[4 * item + 3];
-    const uint32_t p_max = p_min + nrows - 1;
-    const uint32_t n_tiles = p_max / kKT + 1;
-    const uint32_t nblk = p_max / kBS + 1;  // <= kTableLds
-    const uint32_t *table = tables + table_off[seq];
+    const uint32_t slot = blockIdx.x / kv_heads;
+    const uint32_t *descs = plan + num_slots + 1;
+    uint32_t i = plan[slot];
+    const uint32_t i_end = plan[slot + 1];
+    if (i >= i_end) return;  // the host plan gives every slot an item
 
-    const uint32_t tid = threadIdx.x;
-    const uint32_t lane = tid & 63;
-    const uint32_t head = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t c = lane & 31;
-    const uint32_t gl = lane >> 5;
+    const uint32_t head = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t qhead = kvh * G + head;
-    bool row_ok[2];
-    uint32_t p_row[2], wp_min[2];
-#pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
-        row_ok[rg] = kRG * rg + c < nrows;
-        p_row[rg] = p_min + kRG * rg + c;
-        wp_min[rg] = p_min + kRG * rg;
-    }
 
-
-    // DMA: the wave copies 1 KiB (part `head` of 4) of each of the tile's
-    // four blocks, K then V; lane L reads logical unit U of physical unit
-    // P = 64 head + L, as prefill_dma_kernel's stage layout has it.
-    const uint32_t dma_unit = 64 * head + lane;
-    const uint32_t dma_k = (dma_unit ^ ((dma_unit >> 4) & 3u)) * 16;
-    const uint32_t dma_v = (dma_unit ^ ((dma_unit >> 4) & 1u)) * 16;
+    // Per-lane values.  They are rebuilt after the pipelined loop from a
+    // copy of the thread id that the compiler cannot see through, so that
+    // of all of them only that id stays live across the loop's asm (which
+    // leaves 63 VGPRs to the compiler).
+    struct Lane {
+        uint32_t tid, lane, c, gl, dma_k, dma_v, k_rd0, k_rd1, v_rd;
+    };
+    auto make_lane = [&](uint32_t t) __attribute__((always_inline)) {
+        Lane L;
+        L.tid = t;
+        L.lane = t & 63;
+        L.c = L.lane & 31;
+        L.gl = L.lane >> 5;
+        // DMA: the wave copies 1 KiB (part `head` of 4) of each of the
+        // tile's four blocks, K then V; lane L reads logical unit U of
+        // physical unit P = 64 head + L, as prefill_dma_kernel's stage
+        // layout has it.
+        const uint32_t dma_unit = 64 * head + L.lane;
+        L.dma_k = (dma_unit ^ ((dma_unit >> 4) & 3u)) * 16;
+        L.dma_v = (dma_unit ^ ((dma_unit >> 4) & 1u)) * 16;
+        // LDS read offsets within a stage (prefill_dma_kernel's): K A-row c
+        // reads key key_perm(c); V A-row c reads dim 32 dt + c.
+        const uint32_t kp = key_perm(L.c);
+        const uint32_t kx = ((kp & 15) >> 2) & 3;
+        L.k_rd0 = (kp / 16) * kPipeBT + (kp & 15) * 64 + 16 * (L.gl ^ kx);
+        L.k_rd1 = (kp / 16) * kPipeBT + (kp & 15) * 64 + 16 * ((L.gl ^ kx) ^ 2);
+        L.v_rd = 4 * kPipeBT + L.c * 32 + 16 * (L.gl ^ ((L.c >> 3) & 1));
+        return L;
+    };
+    Lane ln = make_lane(threadIdx.x);
     const u32x4 krs = rsrc_words(k_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
     const u32x4 vrs = rsrc_words(v_pool + kvh * kTile, pool_bytes - kvh * kPipeBT);
     const uint32_t stride = kv_heads * kPipeBT;
     const uint32_t st0 = lds_addr(st);
     const uint32_t wbase = st0 + 1024 * head;
-    // LDS DMA of tile t with block byte offsets b into its stage.
-    auto dma_raw = [&](uint32_t t, const uint32_t (&b)[4]) __attribute__((always_inline)) {
-        const uint32_t w = uniform_u32(wbase + (t % 4) * kPipeStage);
+
+    PipeItem A = pipe_item(descs + 4 * i, tables);
+    bool has_b = i + 1 < i_end;
+    PipeItem B = pipe_item(descs + 4 * (has_b ? i + 1 : i), tables);
+    uint32_t T = 0;  // stage of the current item's tile 0
+
+    // LDS DMA of a tile with block byte offsets b into `stage`.
+    auto dma_raw = [&](uint32_t stage, const uint32_t (&b)[4]) __attribute__((always_inline)) {
+        const uint32_t w = uniform_u32(wbase + stage * kPipeStage);
         asm volatile(
             "s_mov_b32 m0, %[w]\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b0] offen lds\n"
             "s_add_u32 m0, %[w], 4096\n s_nop 0\n buffer_load_dwordx4 %[dk], %[krs], %[b1] offen lds\n"
@@ -860,278 +905,341 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             "s_add_u32 m0, %[w], 24576\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b2] offen lds\n"
             "s_add_u32 m0, %[w], 28672\n s_nop 0\n buffer_load_dwordx4 %[dv], %[vrs], %[b3] offen lds\n"
             :
-            : [w] "s"(w), [krs] "s"(krs), [vrs] "s"(vrs), [dk] "v"(dma_k), [dv] "v"(dma_v),
+            : [w] "s"(w), [krs] "s"(krs), [vrs] "s"(vrs), [dk] "v"(ln.dma_k), [dv] "v"(ln.dma_v),
               [b0] "s"(b[0]), [b1] "s"(b[1]), [b2] "s"(b[2]), [b3] "s"(b[3])
             : "m0", "scc", "memory");  // s_add_u32 writes scc
     };
-    // Tile t's block ids from the LDS table (padded: no clamp needed).
+    // The current item's tile t, block ids from the LDS table.
     auto dma = [&](uint32_t t) __attribute__((always_inline)) {
         uint32_t b[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) b[i] = uniform_u32(tbl[4 * t + i]) * stride;
-        dma_raw(t, b);
+        for (int k = 0; k < 4; ++k) b[k] = uniform_u32(tbl[4 * t + k]) * stride;
+        dma_raw((T + t) % 4, b);
     };
-    // The same with the ids read from the sequence's table in global memory
+    // The same with the ids read from the item's table in global memory
     // (scalar loads, clamped to its last block), before the LDS copy exists.
-    auto dma_global = [&](uint32_t t) __attribute__((always_inline)) {
+    auto dma_global = [&](const PipeItem &it, uint32_t t) __attribute__((always_inline)) {
         uint32_t b[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) b[i] = uniform_u32(table[min(4 * t + i, nblk - 1)]) * stride;
-        dma_raw(t, b);
+        for (int k = 0; k < 4; ++k) b[k] = uniform_u32(it.table[min(4 * t + k, it.nblk - 1)]) * stride;
+        dma_raw((T + t) % 4, b);
+    };
+    // The item's block ids into the LDS table, then the next item's first
+    // twelve (or copies of the last id when there is none).
+    auto copy_table = [&](const PipeItem &it, bool has_next, const PipeItem &nx)
+                          __attribute__((always_inline)) {
+        const uint32_t n4 = 4 * it.n_tiles;
+        const uint32_t ntbl = min(n4 + 16, static_cast<uint32_t>(kTableLds + 16));
+        for (uint32_t k = ln.tid; k < ntbl; k += 256)
+            tbl[k] = (k < n4 || !has_next) ? it.table[min(k, it.nblk - 1)]
+                                           : nx.table[min(k - n4, nx.nblk - 1)];
     };
 
-    // The first three tiles' DMA goes out first, so that its latency, the
-    // table copy's and Q's overlap behind one wait.
-    if (fixed_offset) {
-        dma_global(0);
-        dma_global(1);
-        dma_global(2);
-    }
-    {
-        const uint32_t ntbl = min(4 * n_tiles + 16, static_cast<uint32_t>(kTableLds + 16));
-        for (uint32_t i = tid; i < ntbl; i += 256) tbl[i] = table[min(i, nblk - 1)];
-    }
-    if (tid == 0) redo = 0u;
-
+    // Q of an item's rows; a lane past the item's last row loads that row
+    // instead (its results are not stored, and each MFMA column is one
+    // row), so every lane loads and no register is written before its load.
     bf16x8 qv[2][KS];
-#pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
-        const uint16_t *qp =
-            q + (static_cast<uint64_t>(row_begin + kRG * rg + c) * num_heads + qhead) * HD + 8 * gl;
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk)
-            qv[rg][kk] = row_ok[rg] ? __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 16 * kk))
-                                    : bf16x8{};
-    }
-    wait_barrier<0>();  // the table copy, Q and (fixed offset) tiles 0-2
-
-
-    // LDS read offsets within a stage (prefill_dma_kernel's): K A-row c
-    // reads key key_perm(c); V A-row c reads dim 32 dt + c.
-    const uint32_t kp = key_perm(c);
-    const uint32_t kx = ((kp & 15) >> 2) & 3;
-    const uint32_t k_rd0 = (kp / 16) * kPipeBT + (kp & 15) * 64 + 16 * (gl ^ kx);
-    const uint32_t k_rd1 = (kp / 16) * kPipeBT + (kp & 15) * 64 + 16 * ((gl ^ kx) ^ 2);
-    const uint32_t v_rd = 4 * kPipeBT + c * 32 + 16 * (gl ^ ((c >> 3) & 1));
-
-    floatx16 o_acc[2][DT];
-    float m_run[2], l_run[2];
-
-    // One KV tile as ordinary code for both row groups: Q.K^T, the causal mask, the softmax (fixed offset,
-    // or the running max when `running`), P.V.  first: tile 0 (the offset
-    // is its max; P as bf16 hi + lo; the row sum adds the f32 P).
-    auto tile_step = [&](auto first_c, auto running_c, uint32_t t, const bool (&live)[2])
-                         __attribute__((always_inline)) {
-        constexpr bool first = decltype(first_c)::value;
-        constexpr bool running = decltype(running_c)::value;
-        const uint8_t *tile = st + (t % 4) * kPipeStage;
-        const uint32_t j0 = t * kKT;
+    auto load_q = [&](const PipeItem &it) __attribute__((always_inline)) {
 #pragma unroll
         for (int rg = 0; rg < 2; ++rg) {
-            if (!live[rg]) continue;
-            floatx16 s0 = {}, s1 = {};
+            const uint32_t row = it.row_begin + min(kRG * rg + ln.c, it.nrows - 1);
+            const uint16_t *qp = q + (static_cast<uint64_t>(row) * num_heads + qhead) * HD + 8 * ln.gl;
 #pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
-                const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? k_rd1 : k_rd0);
-                const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(tile + off);
-                const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * kPipeBT);
-                s0 = mfma32x32x16(ka, qv[rg][kk], s0);
-                s1 = mfma32x32x16(kb, qv[rg][kk], s1);
-            }
-            float sc[32];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                sc[r] = s0[r];
-                sc[16 + r] = s1[r];
-            }
-            if (j0 + kKT - 1 > wp_min[rg]) {
-#pragma unroll
-                for (int r = 0; r < 32; ++r) {
-                    const uint32_t key = j0 + 32 * (r >> 4) + 16 * ((r >> 3) & 1) + 8 * gl + (r & 7);
-                    sc[r] = (key <= p_row[rg]) ? sc[r] : -INFINITY;
-                }
-            }
-            auto tile_max = [&]() __attribute__((always_inline)) {
-                float mx = sc[0];
-#pragma unroll
-                for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                return mx * scale_log2;
-            };
-            if constexpr (first) {
-                m_run[rg] = tile_max();
-            } else if constexpr (running) {
-                const float mt = tile_max();
-                if (__builtin_amdgcn_ballot_w64(mt > m_run[rg] + kLazyLog2) != 0) {
-                    const float m_new = fmaxf(m_run[rg], mt);
-                    const float alpha = __builtin_amdgcn_exp2f(m_run[rg] - m_new);
-                    l_run[rg] *= alpha;
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] *= alpha;
-                    m_run[rg] = m_new;
-                }
-            }
-            const float nm = -m_run[rg];
-#pragma unroll
-            for (int r = 0; r < 32; ++r) sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, nm));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                bf16x8 pb_hi, pb_lo;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float p = sc[16 * (j >> 1) + 8 * (j & 1) + i];
-                    const __bf16 hi = static_cast<__bf16>(p);
-                    pb_hi[i] = hi;
-                    if constexpr (first) pb_lo[i] = static_cast<__bf16>(p - static_cast<float>(hi));
-                    l_run[rg] += p;
-                }
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const bf16x8 vf =
-                        *reinterpret_cast<const bf16x8 *>(tile + v_rd + j * kPipeBT + dt * 1024);
-                    if constexpr (first) o_acc[rg][dt] = mfma32x32x16(vf, pb_lo, o_acc[rg][dt]);
-                    o_acc[rg][dt] = mfma32x32x16(vf, pb_hi, o_acc[rg][dt]);
-                }
-            }
+            for (int kk = 0; kk < KS; ++kk)
+                qv[rg][kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(qp + 16 * kk));
         }
     };
+
+    // The first item: its first three tiles' DMA goes out first, so that
+    // its latency, the table copy's and Q's overlap behind one wait.
+    if (fixed_offset) {
+        dma_global(A, 0);
+        dma_global(A, 1);
+        dma_global(A, 2);
+    }
+    copy_table(A, has_b, B);
+    if (ln.tid == 0) {
+        redo[0] = 0u;
+        redo[1] = 0u;
+    }
+    load_q(A);
+    wait_barrier<0>();  // the table copy, Q and (fixed offset) tiles 0-2
+    // Tiles 0-2 of the current item are in their stages (issued and waited
+    // for, or in flight from the previous item's DMAs past its end).
+    bool ready = fixed_offset != 0;
 
     using True = std::true_type;
     using False = std::false_type;
-
-    // One pass as ordinary code, for the row groups in `live`: running max
-    // (the recompute) or the fixed offset (when the pipelined loop is off).
-    auto plain_pass = [&](auto running_c, const bool (&live)[2]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-            if (!live[rg]) continue;
-            m_run[rg] = 0.0f;
-            l_run[rg] = 0.0f;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
-        }
-        dma(0);
-        dma(1);
-        dma(2);
-        wait_barrier<16>();
-        dma(3);
-        tile_step(True{}, running_c, 0, live);
-        for (uint32_t t = 1; t < n_tiles; ++t) {
-            wait_barrier<16>();
-            dma(t + 3);
-            tile_step(False{}, running_c, t, live);
-        }
-        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0): the DMA past the end
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
-            if (live[rg]) l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
-    };
-
     const bool both[2] = {true, true};
-    if (fixed_offset) {
-        // Tile 0 here, tiles 1 .. n - 1 in the pipelined loop.
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-            l_run[rg] = 0.0f;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
-        }
-        dma(3);
-        tile_step(True{}, False{}, 0, both);
-        if (n_tiles >= 2) {
-            // Tiles from `tmask` (a key index) on need the causal mask: the
-            // first is the one holding row group 0's first row's last
-            // visible key + 1.
-            const uint32_t tmask = kKT * ((p_min + 1) / kKT);
-            float nm0 = -m_run[0], nm1 = -m_run[1];
-            uint32_t vtbl = lds_addr(tbl) + 16 * 4;  // the ids of tile 4
-            const int32_t pr0 = static_cast<int32_t>(p_row[0] - 8 * gl);
-            const int32_t pr1 = static_cast<int32_t>(p_row[1] - 8 * gl);
-            uint32_t t_reg, j0_reg, b0, b1, b2, b3;
-            uint64_t mk0, mk1, mk2;
-            asm volatile(VO_PREFILL_PIPE_LOOP
-                         : "+{a[0:15]}"(o_acc[0][0]), "+{a[16:31]}"(o_acc[0][1]),
-                           "+{a[32:47]}"(o_acc[0][2]), "+{a[48:63]}"(o_acc[0][3]),
-                           "+{a[64:79]}"(o_acc[1][0]), "+{a[80:95]}"(o_acc[1][1]),
-                           "+{a[96:111]}"(o_acc[1][2]), "+{a[112:127]}"(o_acc[1][3]),
-                           "+{v166}"(l_run[0]), "+{v167}"(l_run[1]), "+{v189}"(vtbl),
-                           [t] "=&s"(t_reg), [j0] "=&s"(j0_reg), [b0] "=&s"(b0), [b1] "=&s"(b1),
-                           [b2] "=&s"(b2), [b3] "=&s"(b3), [m0] "=&s"(mk0), [m1] "=&s"(mk1),
-                           [m2] "=&s"(mk2)
-                         : "{a[128:131]}"(qv[0][0]), "{a[132:135]}"(qv[0][1]),
-                           "{a[136:139]}"(qv[0][2]), "{a[140:143]}"(qv[0][3]),
-                           "{a[144:147]}"(qv[0][4]), "{a[148:151]}"(qv[0][5]),
-                           "{a[152:155]}"(qv[0][6]), "{a[156:159]}"(qv[0][7]),
-                           "{a[160:163]}"(qv[1][0]), "{a[164:167]}"(qv[1][1]),
-                           "{a[168:171]}"(qv[1][2]), "{a[172:175]}"(qv[1][3]),
-                           "{a[176:179]}"(qv[1][4]), "{a[180:183]}"(qv[1][5]),
-                           "{a[184:187]}"(qv[1][6]), "{a[188:191]}"(qv[1][7]),
-                           "{v164}"(nm0), "{v165}"(nm1),
-                           "{v181}"(st0 + k_rd0), "{v182}"(st0 + k_rd1), "{v185}"(st0 + v_rd),
-                           "{v187}"(dma_k), "{v188}"(dma_v), "{v190}"(pr0), "{v191}"(pr1), [krs] "s"(krs),
-                           [vrs] "s"(vrs), [wbase] "s"(wbase), [stride] "s"(stride),
-                           [tend] "s"(n_tiles), [tmask] "s"(tmask), [scale] "s"(scale_log2)
-                         : VO_PREFILL_PIPE_CLOBBERS, "m0", "scc", "memory");
-        }
-        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-#pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
-            l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
-            const bool ok = l_run[rg] < kOverflowSum && all_finite(o_acc[rg]);  // false for inf, NaN
-            if (__builtin_amdgcn_ballot_w64(row_ok[rg] && !ok) != 0 && lane == 0)
-                atomicOr(&redo, 1u << rg);
-        }
-    } else if (tid == 0) {
-        redo = 3u;
-    }
-    wait_barrier<0>();
-    const uint32_t again = uniform_u32(redo);
-    if (again != 0) {
-        // The recompute with the running max for the 32-row groups that
-        // left the fixed-offset range (prefill_dma_kernel's second pass).
-        const bool live[2] = {(again & 1u) != 0, (again & 2u) != 0};
-        wait_barrier<0>();
-        plain_pass(True{}, live);
-    }
-    wait_barrier<0>();
 
-    // Output through LDS, as prefill_dma_kernel: the tile of (row group rg,
-    // head h) is tile 4 rg + h, 8 KiB each, chunk q of row c at q ^ (c % 16).
-    constexpr int ROWB = HD * 2;
-    constexpr int CH = HD / 8;
-    constexpr int WTILE = kRG * ROWB;
+    for (uint32_t k_item = 0;; ++k_item) {
+        const uint32_t n_tiles = A.n_tiles;
+        uint32_t *const my_redo = &redo[k_item & 1];
+        if (ln.tid == 0) redo[(k_item + 1) & 1] = 0u;
+
+        floatx16 o_acc[2][DT];
+        float m_run[2], l_run[2];
+
+        // One KV tile as ordinary code for both row groups: Q.K^T, the
+        // causal mask, the softmax (fixed offset, or the running max when
+        // `running`), P.V.  first: tile 0 (the offset is its max; P as bf16
+        // hi + lo; the row sum adds the f32 P).
+        auto tile_step = [&](auto first_c, auto running_c, uint32_t t, const bool (&live)[2])
+                             __attribute__((always_inline)) {
+            constexpr bool first = decltype(first_c)::value;
+            constexpr bool running = decltype(running_c)::value;
+            const uint8_t *tile = st + ((T + t) % 4) * kPipeStage;
+            const uint32_t j0 = t * kKT;
 #pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
-        const float inv = 1.0f / l_run[rg];
-        uint8_t *tile = st + (4 * rg + head) * WTILE + c * ROWB + 8 * gl;
+            for (int rg = 0; rg < 2; ++rg) {
+                if (!live[rg]) continue;
+                const uint32_t p_row = A.p_min + kRG * rg + ln.c;
+                const uint32_t wp_min = A.p_min + kRG * rg;
+                floatx16 s0 = {}, s1 = {};
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+                for (int kk = 0; kk < KS; ++kk) {
+                    const uint32_t off = (kk / 2) * (kBS * 64) + ((kk & 1) ? ln.k_rd1 : ln.k_rd0);
+                    const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(tile + off);
+                    const bf16x8 kb = *reinterpret_cast<const bf16x8 *>(tile + off + 2 * kPipeBT);
+                    s0 = mfma32x32x16(ka, qv[rg][kk], s0);
+                    s1 = mfma32x32x16(kb, qv[rg][kk], s1);
+                }
+                float sc[32];
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                u32x2 packed;
-                packed[0] = f32_to_bf16_bits(o_acc[rg][dt][4 * r4] * inv) |
-                            (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[rg][dt][4 * r4 + 1] * inv)) << 16);
-                packed[1] = f32_to_bf16_bits(o_acc[rg][dt][4 * r4 + 2] * inv) |
-                            (static_cast<uint32_t>(f32_to_bf16_bits(o_acc[rg][dt][4 * r4 + 3] * inv)) << 16);
-                const uint32_t q4 = static_cast<uint32_t>(4 * dt + r4) ^ (c % CH);
-                *reinterpret_cast<u32x2 *>(tile + 16 * q4) = packed;
+                for (int r = 0; r < 16; ++r) {
+                    sc[r] = s0[r];
+                    sc[16 + r] = s1[r];
+                }
+                if (j0 + kKT - 1 > wp_min) {
+#pragma unroll
+                    for (int r = 0; r < 32; ++r) {
+                        const uint32_t key = j0 + 32 * (r >> 4) + 16 * ((r >> 3) & 1) + 8 * ln.gl + (r & 7);
+                        sc[r] = (key <= p_row) ? sc[r] : -INFINITY;
+                    }
+                }
+                auto tile_max = [&]() __attribute__((always_inline)) {
+                    float mx = sc[0];
+#pragma unroll
+                    for (int r = 1; r < 32; ++r) mx = fmaxf(mx, sc[r]);
+                    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                    return mx * scale_log2;
+                };
+                if constexpr (first) {
+                    m_run[rg] = tile_max();
+                } else if constexpr (running) {
+                    const float mt = tile_max();
+                    if (__builtin_amdgcn_ballot_w64(mt > m_run[rg] + kLazyLog2) != 0) {
+                        const float m_new = fmaxf(m_run[rg], mt);
+                        const float alpha = __builtin_amdgcn_exp2f(m_run[rg] - m_new);
+                        l_run[rg] *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] *= alpha;
+                        m_run[rg] = m_new;
+                    }
+                }
+                const float nm = -m_run[rg];
+#pragma unroll
+                for (int r = 0; r < 32; ++r) sc[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], scale_log2, nm));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    bf16x8 pb_hi, pb_lo;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float p = sc[16 * (j >> 1) + 8 * (j & 1) + e];
+                        const __bf16 hi = static_cast<__bf16>(p);
+                        pb_hi[e] = hi;
+                        if constexpr (first) pb_lo[e] = static_cast<__bf16>(p - static_cast<float>(hi));
+                        l_run[rg] += p;
+                    }
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        const bf16x8 vf =
+                            *reinterpret_cast<const bf16x8 *>(tile + ln.v_rd + j * kPipeBT + dt * 1024);
+                        if constexpr (first) o_acc[rg][dt] = mfma32x32x16(vf, pb_lo, o_acc[rg][dt]);
+                        o_acc[rg][dt] = mfma32x32x16(vf, pb_hi, o_acc[rg][dt]);
+                    }
+                }
+            }
+        };
+
+        // One pass as ordinary code, for the row groups in `live`: running
+        // max (the recompute) or the fixed offset (when the pipelined loop
+        // is off).  Its tiles 0-2 are issued here; the caller has waited for
+        // every DMA in flight.
+        auto plain_pass = [&](auto running_c, const bool (&live)[2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg) {
+                if (!live[rg]) continue;
+                m_run[rg] = 0.0f;
+                l_run[rg] = 0.0f;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o_acc[rg][dt] = floatx16{};
+            }
+            dma(0);
+            dma(1);
+            dma(2);
+            wait_barrier<16>();
+            dma(3);
+            tile_step(True{}, running_c, 0, live);
+            for (uint32_t t = 1; t < n_tiles; ++t) {
+                wait_barrier<16>();
+                dma(t + 3);
+                tile_step(False{}, running_c, t, live);
+            }
+            // vmcnt(0): the DMA past the end (the next item's tiles 0-2)
+            __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg)
+                if (live[rg]) l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
+        };
+
+        // Tiles nA .. nA + 2 of this item's ring positions carry the next
+        // item's tiles 0-2 when each was issued from the LDS table.
+        bool next_ready = true;
+        if (fixed_offset) {
+            // Tile 0 here, tiles 1 .. n - 1 in the pipelined loop.
+            if (!ready) {
+                dma(0);
+                dma(1);
+                dma(2);
+                wait_barrier<0>();
+            }
+            next_ready = n_tiles >= 3 || !ready;
+            {
+                // The whole item in the generated code: tile 0 (its max
+                // becomes the fixed offset), then tiles 1 .. n - 1.  Tiles
+                // from `tmask` (a key index) on need the causal mask: the
+                // first is the one holding row group 0's first row's last
+                // visible key + 1.
+                l_run[0] = 0.0f;
+                l_run[1] = 0.0f;
+                const uint32_t tmask = kKT * ((A.p_min + 1) / kKT);
+                const uint32_t tend = T + n_tiles;
+                uint32_t vtbl = lds_addr(tbl) + 16 * 3;  // the ids of tile 3
+                const int32_t pr0 = static_cast<int32_t>(A.p_min + ln.c - 8 * ln.gl);
+                const int32_t pr1 = static_cast<int32_t>(A.p_min + kRG + ln.c - 8 * ln.gl);
+                uint32_t t_reg, j0_reg, b0, b1, b2, b3;
+                uint64_t mk0, mk1, mk2;
+                asm volatile(VO_PREFILL_PIPE_LOOP
+                             : "={a[0:15]}"(o_acc[0][0]), "={a[16:31]}"(o_acc[0][1]),
+                               "={a[32:47]}"(o_acc[0][2]), "={a[48:63]}"(o_acc[0][3]),
+                               "={a[64:79]}"(o_acc[1][0]), "={a[80:95]}"(o_acc[1][1]),
+                               "={a[96:111]}"(o_acc[1][2]), "={a[112:127]}"(o_acc[1][3]),
+                               "+{v166}"(l_run[0]), "+{v167}"(l_run[1]), "+{v189}"(vtbl),
+                               [t] "=&s"(t_reg), [j0] "=&s"(j0_reg), [b0] "=&s"(b0), [b1] "=&s"(b1),
+                               [b2] "=&s"(b2), [b3] "=&s"(b3), [m0] "=&s"(mk0), [m1] "=&s"(mk1),
+                               [m2] "=&s"(mk2)
+                             : "{a[128:131]}"(qv[0][0]), "{a[132:135]}"(qv[0][1]),
+                               "{a[136:139]}"(qv[0][2]), "{a[140:143]}"(qv[0][3]),
+                               "{a[144:147]}"(qv[0][4]), "{a[148:151]}"(qv[0][5]),
+                               "{a[152:155]}"(qv[0][6]), "{a[156:159]}"(qv[0][7]),
+                               "{a[160:163]}"(qv[1][0]), "{a[164:167]}"(qv[1][1]),
+                               "{a[168:171]}"(qv[1][2]), "{a[172:175]}"(qv[1][3]),
+                               "{a[176:179]}"(qv[1][4]), "{a[180:183]}"(qv[1][5]),
+                               "{a[184:187]}"(qv[1][6]), "{a[188:191]}"(qv[1][7]),
+                               "{v181}"(st0 + ln.k_rd0), "{v182}"(st0 + ln.k_rd1), "{v185}"(st0 + ln.v_rd),
+                               "{v187}"(ln.dma_k), "{v188}"(ln.dma_v), "{v190}"(pr0), "{v191}"(pr1),
+                               [krs] "s"(krs), [vrs] "s"(vrs), [wbase] "s"(wbase), [stride] "s"(stride),
+                               [tbase] "s"(T), [tend] "s"(tend), [tmask] "s"(tmask),
+                               [scale] "s"(scale_log2)
+                             : VO_PREFILL_PIPE_CLOBBERS, "m0", "scc", "memory");
+                uint32_t t2 = ln.tid;
+                asm volatile("" : "+v"(t2));
+                ln = make_lane(t2);
+            }
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg) {
+                l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
+                const bool ok = l_run[rg] < kOverflowSum && all_finite(o_acc[rg]);  // false for inf, NaN
+                if (__builtin_amdgcn_ballot_w64(kRG * rg + ln.c < A.nrows && !ok) != 0 && ln.lane == 0)
+                    atomicOr(my_redo, 1u << rg);
+            }
+        } else if (ln.tid == 0) {
+            *my_redo = 3u;
+        }
+        wait_barrier<63>();  // the flags; every wave is done with this item's tiles
+        const uint32_t again = uniform_u32(*my_redo);
+        if (again != 0) {
+            // The recompute with the running max for the 32-row groups that
+            // left the fixed-offset range (prefill_dma_kernel's second pass),
+            // after the DMAs in flight (the next item's tiles) have landed.
+            const bool live[2] = {(again & 1u) != 0, (again & 2u) != 0};
+            wait_barrier<0>();
+            plain_pass(True{}, live);
+            next_ready = true;
+            wait_barrier<63>();  // every wave is done with the stages
+        }
+
+        // The next item's Q (this item's is no longer needed).
+        bool has_c = false;
+        PipeItem C = B;
+        if (has_b) {
+            load_q(B);
+            has_c = i + 2 < i_end;
+            C = pipe_item(descs + 4 * (has_c ? i + 2 : i + 1), tables);
+        }
+
+        // Output: each wave its own head's rows, one row group at a time,
+        // through 8 KiB of the stage that holds no prefetched tile (this
+        // item's last tile's); chunk q of row c at q ^ (c % 16).  The stores
+        // are non-temporal: the output is not read again by this kernel, and
+        // lines left dirty in L2 are written back when the kernel ends.
+        {
+            constexpr int ROWB = HD * 2;
+            constexpr int CH = HD / 8;
+            uint8_t *wst = st + ((T + n_tiles + 3) % 4) * kPipeStage + head * (kRG * ROWB);
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg) {
+                const float inv = 1.0f / l_run[rg];
+                uint8_t *row_at = wst + ln.c * ROWB + 8 * ln.gl;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        bf16x4 packed;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            packed[e] = static_cast<__bf16>(o_acc[rg][dt][4 * r4 + e] * inv);
+                        const uint32_t q4 = static_cast<uint32_t>(4 * dt + r4) ^ (ln.c % CH);
+                        *reinterpret_cast<bf16x4 *>(row_at + 16 * q4) = packed;
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                uint16_t *obase = out + (static_cast<uint64_t>(A.row_begin + kRG * rg) * num_heads + qhead) * HD;
+#pragma unroll
+                for (int k = 0; k < kRG * CH / 64; ++k) {
+                    const uint32_t idx = ln.lane + 64 * k;
+                    const uint32_t row = idx / CH;
+                    const uint32_t q4 = idx % CH;
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wst + row * ROWB + 16 * (q4 ^ (row % CH)));
+                    if (kRG * rg + row < A.nrows)
+                        __builtin_nontemporal_store(
+                            v, reinterpret_cast<u32x4 *>(obase + static_cast<uint64_t>(row) * num_heads * HD + 8 * q4));
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             }
         }
+        if (!has_b) break;
+        // The next item: its table (and the first ids of the one after),
+        // then one wait for its Q, its table and its tiles 0-2; the barrier
+        // also orders every wave's output reads before the DMA of its tile 3
+        // rewrites that stage.
+        copy_table(B, has_c, C);
+        T = (T + n_tiles) % 4;
+        wait_barrier<0>();
+        ready = next_ready;
+        A = B;
+        B = C;
+        has_b = has_c;
+        ++i;
     }
-    wait_barrier<0>();
-    constexpr uint32_t kRowChunks = G * CH;
-    uint16_t *obase = out + (static_cast<uint64_t>(row_begin) * num_heads + kvh * G) * HD;
-    for (uint32_t k = tid; k < nrows * kRowChunks; k += 256) {
-        const uint32_t row = k / kRowChunks;
-        const uint32_t h = (k % kRowChunks) / CH;
-        const uint32_t q4 = k % CH;
-        const uint32_t w = h + G * (row / kRG);
-        const uint32_t cr = row % kRG;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(st + w * WTILE + cr * ROWB +
-                                                         16 * (q4 ^ (cr % CH)));
-        *reinterpret_cast<u32x4 *>(obase + static_cast<uint64_t>(row) * num_heads * HD + h * HD +
-                                   8 * q4) = v;
-    }
+    // The last item's DMAs past its end write LDS: they land before the
+    // workgroup ends.
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
 }
 
 // VO_PREFILL_STAGING=regs selects the register-staged kernel above (A/B).
@@ -1196,13 +1304,13 @@ hipError_t launch_gr(const PoolLayer &pool, const MetaView &meta, const PrefillP
     }
     if constexpr (HD == 128 && G == 4 && R == 2) {
         // 64-row workgroups at the Llama-3-8B shape: the pipelined kernel.
-        if (regs_items < plan.num_items && prefill_pipe_enabled()) {
+        if (regs_items < plan.num_items && plan.pipe != nullptr && plan.pipe_slots != 0 &&
+            prefill_pipe_enabled()) {
             KernelTimer timer("prefill_pipe", stream);
-            hipLaunchKernelGGL(prefill_pipe_kernel, dim3((plan.num_items - regs_items) * per_item),
-                               dim3(256), 0, stream, pool.k, pool.v, pool.kv_heads, meta.table_off,
-                               meta.tables, plan.work + 4 * static_cast<uint64_t>(regs_items), q,
-                               out, num_heads, scale_log2, prefill_fixed_offset() ? 1u : 0u,
-                               static_cast<uint32_t>(pool.elems * 2));
+            hipLaunchKernelGGL(prefill_pipe_kernel, dim3(plan.pipe_slots * pool.kv_heads), dim3(256), 0,
+                               stream, pool.k, pool.v, pool.kv_heads, meta.tables, plan.pipe,
+                               plan.pipe_slots, q, out, num_heads, scale_log2,
+                               prefill_fixed_offset() ? 1u : 0u, static_cast<uint32_t>(pool.elems * 2));
             return hipGetLastError();
         }
     }

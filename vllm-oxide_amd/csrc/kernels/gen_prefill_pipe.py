@@ -6,8 +6,12 @@
 One wavefront per SIMD holds 64 query rows (row groups rg 0 and 1, 32 rows
 each) of one query head, head_dim 128.  Tile 0 runs before the loop (its
 max is the fixed softmax offset m); the loop covers tiles 1 .. n - 1.
-Before the loop, the fill computes S of tile 1 (masked if needed) and P of
-its first 16 keys.  Iteration t then issues, in MFMA order,
+Tile t of the item sits in LDS stage (tbase + t) % 4: the persistent kernel
+runs several items back to back through one ring, and an item's tile 0
+follows the previous item's last tile.  The tile counter t of the loop is
+tbase + (the tile's index in the item); keys are indexed from the item's
+first key.  Before the loop, the fill computes S of tile 1 (masked if
+needed) and P of its first 16 keys.  Iteration t then issues, in MFMA order,
 
     P1  P.V of tile t, keys 0-15   ( 8 MFMAs; V fragments and P ready)
     P2  Q.K^T of tile t + 1        (32 MFMAs; K from LDS stage (t+1) % 4)
@@ -22,7 +26,10 @@ instructions co-issue with a running 32-cycle v_mfma_f32_32x32x16_bf16, so
 the softmax runs under the MFMAs.  Iteration t starts with the wait for tile
 t + 1's DMA and a barrier (after which stage (t+3) % 4 is free: every wave
 has left iteration t - 1), then issues the DMA of tile t + 3 under P1's
-MFMAs.  The last tile (t = n - 1) takes a variant without Q.K^T.
+MFMAs.  The last tile (t = n - 1) takes a variant without Q.K^T; its DMA,
+like those of the two iterations before it, fetches a tile past the item's
+end: the block table in LDS continues there with the next item's first
+three tiles, which so arrive while this item finishes.
 
 Each K or V fragment read from LDS feeds two MFMAs (the two row groups).
 Per row the arithmetic is the 32-row kernels' operation for operation: S
@@ -216,7 +223,7 @@ class Body:
 # slot is filled to 28 cycles first (probe of this loop with static LDS,
 # MFMA floor 2,176): co-issued VALU still costs about a cycle per op, more
 # when bunched.
-COST = {"v_exp_f32": 9, "s_nop": 2}
+COST = {"v_exp_f32": 9, "s_nop": 2, "WAITALL": 0}
 BUDGET = 16
 
 
@@ -246,16 +253,20 @@ def run_slots(b, mfmas, reads, valu, side, first_use):
             ri += 1
 
     def put_valu(op):
+        if op == "WAITALL":
+            b.emit("s_waitcnt lgkmcnt(0)")
+            b.lds_done = b.lds_n
+            return
         b.emit(op)
         if op.startswith("v_cvt_pk_bf16_f32"):
             reg = int(op.split()[1].rstrip(",")[1:])
-            last_pack[reg - (reg - 128) % 4] = len(b.lines)
+            last_pack[reg - reg % 4] = len(b.lines)
 
     for slot, (text, rkey, pneed) in enumerate(mfmas):
         k = 0
         while si < len(side) and side[si][1] <= slot and k < 6:
             op = side[si][0]
-            if op.startswith("ds_read"):
+            if op.startswith("ds_"):
                 b.lds(op)
             else:
                 b.emit(op)
@@ -284,7 +295,7 @@ def run_slots(b, mfmas, reads, valu, side, first_use):
             emitted += 1
     while si < len(side):
         op = side[si][0]
-        if op.startswith("ds_read"):
+        if op.startswith("ds_"):
             b.lds(op)
         else:
             b.emit(op)
@@ -308,7 +319,8 @@ def dma_side(stage_dma):
 
 def iteration(stage, masked_next, last):
     """Tile t with t % 4 == stage.  masked_next: tile t + 1 needs the causal
-    mask.  last: t is the last tile (no Q.K^T of a next tile, no DMA)."""
+    mask.  last: t is the last tile (no Q.K^T of a next tile, no block ids
+    to read)."""
     b = Body()
     cur, nxt = stage % 2, (stage + 1) % 2
     kst = (stage + 1) % 4
@@ -338,9 +350,8 @@ def iteration(stage, masked_next, last):
     if not last:
         reads += [(("k", n), k_read(kst, n), K_AHEAD) for n in range(16)]
     reads += [(("v", nv), v_read(stage, nv), V_AHEAD) for nv in range(4, 16)]
-    side = []
+    side = [(op, 0) for op in dma_side((stage + 3) % 4)]
     if not last:
-        side += [(op, 0) for op in dma_side((stage + 3) % 4)]
         side += [("ds_read_b128 v[160:163], v189", 1), ("v_add_u32 v189, 16, v189", 1)]
         # the next tile's first V fragments, once slots 0-3 (fragments
         # 8-11 of this tile) have been read by their MFMAs
@@ -358,10 +369,12 @@ def iteration(stage, masked_next, last):
     return b.lines
 
 
-def fill(masked):
-    """Before iteration 1: tile 1 has landed (vmcnt(16): tiles 2 and 3 in
-    flight); ids of tile 4; Q.K^T of tile 1 into S buffer 1, its mask if
-    needed, P of its keys 0-15, and its first V fragments."""
+def fill(stage, masked):
+    """Before iteration 1, tile 1 in `stage`: tile 1 has landed (vmcnt(16):
+    tiles 2 and 3 in flight); ids of tile 4; Q.K^T of tile 1 into S buffer
+    stage % 2, its mask if needed, P of its keys 0-15, and its first V
+    fragments."""
+    buf = stage % 2
     b = Body()
     b.emit("s_waitcnt vmcnt(16) lgkmcnt(0)")
     b.emit("s_barrier")
@@ -369,16 +382,181 @@ def fill(masked):
     for n in range(16):
         for rg in range(2):
             first_use.setdefault(("k", n), len(mfmas))
-            mfmas.append((qk_mfma(1, n, rg), ("k", n), []))
-    reads = [(("k", n), k_read(1, n), K_AHEAD) for n in range(16)]
+            mfmas.append((qk_mfma(buf, n, rg), ("k", n), []))
+    reads = [(("k", n), k_read(stage, n), K_AHEAD) for n in range(16)]
     side = [("ds_read_b128 v[160:163], v189", 0), ("v_add_u32 v189, 16, v189", 0)]
     run_slots(b, mfmas, reads, [], side, first_use)
     b.lines += ["s_nop 7", "s_nop 7", "s_nop 7"]
     if masked:
-        b.lines += mask_ops(1)
-    b.lines += softmax_j(1, 0)
+        b.lines += mask_ops(buf)
+    b.lines += softmax_j(buf, 0)
     for nv in range(4):
-        b.lds(v_read(1, nv))
+        b.lds(v_read(stage, nv))
+    return b.lines
+
+
+
+def max_ops(buf):
+    """Row max of tile 0's scores (S buffer `buf`, masked): per lane and row
+    group a tree of v_max_f32 over its 32 scores into the P registers (free
+    until tile 0's packs), the address of lane ^ 32 for the exchange (v192),
+    and, after the exchange, -max * scale into v164 / v165."""
+    tree = []
+    for rg in range(2):
+        t = 128 + 16 * rg
+        src = [S(buf, rg, h) + r for h in range(2) for r in range(16)]
+        lvl = [(f"v_max_f32 v{t + i}, v{src[2 * i]}, v{src[2 * i + 1]}", rg) for i in range(16)]
+        tree.append(lvl)
+    ops = []
+    # level 1 of both row groups interleaved, then the in-place levels
+    for i in range(16):
+        for rg in range(2):
+            ops.append(tree[rg][i][0])
+    n = 16
+    while n > 1:
+        n //= 2
+        for i in range(n):
+            for rg in range(2):
+                t = 128 + 16 * rg
+                ops.append(f"v_max_f32 v{t + i}, v{t + 2 * i}, v{t + 2 * i + 1}")
+    ops += ["v_mbcnt_lo_u32_b32 v192, -1, 0", "v_mbcnt_hi_u32_b32 v192, -1, v192",
+            "v_xor_b32 v192, 32, v192", "v_lshlrev_b32 v192, 2, v192"]
+    return ops
+
+
+def exchange_side():
+    return ["ds_bpermute_b32 v130, v192, v128", "ds_bpermute_b32 v146, v192, v144"]
+
+
+def nm_ops():
+    return ["WAITALL", "v_max_f32 v128, v128, v130", "v_max_f32 v144, v144, v146",
+            "v_mul_f32_e64 v164, -v128, %[scale]", "v_mul_f32_e64 v165, -v144, %[scale]"]
+
+
+def LO(buf, rg, j):
+    """Tile 0's bf16 lo packs of (rg, j): the first four registers of the
+    eight scores they come from."""
+    return S(buf, rg, j >> 1) + 8 * (j & 1)
+
+
+def softmax0_j(buf, j):
+    """Tile 0's softmax of 16-key step j: p = exp2(fma(s, scale, -m)), the
+    row sum adds p in key order, P as bf16 hi (P registers) + lo, lo =
+    bf16(p - hi) (the hi as f32 from its pack; v192 / v193 as scratch for
+    row group 0 / 1)."""
+    ops = []
+    base = [LO(buf, rg, j) for rg in range(2)]
+    for i in range(8):
+        for rg in range(2):
+            ops.append(f"v_fma_f32 v{base[rg] + i}, v{base[rg] + i}, %[scale], v{164 + rg}")
+            ops.append(f"v_exp_f32 v{base[rg] + i}, v{base[rg] + i}")
+    for k in range(4):
+        for rg in range(2):
+            b, hi, tmp = base[rg], P(rg, j) + k, 192 + rg
+            ops += [f"v_add_f32 v{166 + rg}, v{166 + rg}, v{b + 2 * k}",
+                    f"v_add_f32 v{166 + rg}, v{166 + rg}, v{b + 2 * k + 1}",
+                    f"v_cvt_pk_bf16_f32 v{hi}, v{b + 2 * k}, v{b + 2 * k + 1}",
+                    f"v_lshlrev_b32 v{tmp}, 16, v{hi}",
+                    f"v_sub_f32 v{b + 2 * k}, v{b + 2 * k}, v{tmp}",
+                    f"v_and_b32 v{tmp}, 0xffff0000, v{hi}",
+                    f"v_sub_f32 v{b + 2 * k + 1}, v{b + 2 * k + 1}, v{tmp}",
+                    f"v_cvt_pk_bf16_f32 v{b + k}, v{b + 2 * k}, v{b + 2 * k + 1}"]
+    return ops
+
+
+def pv0_mfma(n, rg, buf, lo):
+    """P.V of tile 0 for V fragment n = 4 j + dt: P lo (first, from zero at
+    j = 0) or hi."""
+    j, dt = n // 4, n % 4
+    preg = LO(buf, rg, j) if lo else P(rg, j)
+    src_c = "0" if (lo and j == 0) else O(rg, dt)
+    return f"v_mfma_f32_32x32x16_bf16 {O(rg, dt)}, {vslot(n)}, v[{preg}:{preg + 3}], {src_c}", preg
+
+
+def head(stage, single):
+    """Tile 0 (in `stage`) of the item, and unless `single` the start of
+    tile 1: the DMA of tile 3; Q.K^T of tile 0; Q.K^T of tile 1 with tile
+    0's mask, max and softmax (P as hi + lo) under it; P.V of tile 0 (lo,
+    then hi, per 16-key step) with tile 1's mask and the P of its keys 0-15
+    under it; tile 1's first V fragments.  Tiles 0 and 1 always take the
+    causal mask (it keeps every key a row sees).  Leaves the state the loop
+    expects at tile 1 (or, single, the item's result)."""
+    b = Body()
+    b0 = stage % 2
+    st1 = (stage + 1) % 4
+    b1 = st1 % 2
+    # the ids of tile 3, its DMA, then the ids of tile 4
+    seq = b.lds("ds_read_b128 v[160:163], v189")
+    b.emit("v_add_u32 v189, 16, v189")
+    b.wait(seq)
+    b.lines += dma_side((stage + 3) % 4)
+    b.lds("ds_read_b128 v[160:163], v189")
+    b.emit("v_add_u32 v189, 16, v189")
+    b.emit("s_mov_b32 %[j0], 0")
+    mfmas, first_use, reads = [], {}, []
+    for n in range(16):
+        for rg in range(2):
+            first_use.setdefault(("k0", n), len(mfmas))
+            mfmas.append((qk_mfma(b0, n, rg), ("k0", n), []))
+    reads += [(("k0", n), k_read(stage, n), K_AHEAD) for n in range(16)]
+    z1 = len(mfmas)
+    if not single:
+        for n in range(16):
+            for rg in range(2):
+                first_use.setdefault(("k1", n), len(mfmas))
+                mfmas.append((qk_mfma(b1, n, rg), ("k1", n), []))
+        reads += [(("k1", n), k_read(st1, n), K_AHEAD) for n in range(16)]
+    z3 = len(mfmas)
+    if single:
+        # nothing to overlap tile 0's softmax with
+        run_slots(b, mfmas, reads, [], [], first_use)
+        b.lines += ["s_nop 7", "s_nop 7", "s_nop 7"]
+        b.lines += mask_ops(b0)
+        b.lines += max_ops(b0)
+        for op in exchange_side():
+            b.lds(op)
+        for op in nm_ops():
+            if op == "WAITALL":
+                b.emit("s_waitcnt lgkmcnt(0)")
+                b.lds_done = b.lds_n
+            else:
+                b.emit(op)
+        for j in range(4):
+            b.lines += softmax0_j(b0, j)
+        b.lines += ["s_nop 1"]
+        mfmas, first_use, reads = [], {}, []
+        z3 = 0
+    pv = []
+    for j in range(4):
+        for lo in (True, False):
+            for dt in range(4):
+                for rg in range(2):
+                    n = 4 * j + dt
+                    text, preg = pv0_mfma(n, rg, b0, lo)
+                    first_use.setdefault(("v0", n), len(mfmas))
+                    mfmas.append((text, ("v0", n), [preg]))
+    reads += [(("v0", n), v_read(stage, n), V_AHEAD) for n in range(16)]
+    end = len(mfmas)
+    valu, side = [], []
+    if not single:
+        ready0 = z1 + 3  # three MFMAs after the last Q.K^T of tile 0
+        mx = mask_ops(b0) + max_ops(b0)
+        xs = ready0 + 20  # the exchange, once the tree is done
+        valu += [(op, ready0, xs - 1) for op in mx]
+        side += [(op, xs) for op in exchange_side()]
+        valu += [(op, xs + 2, z3) for op in nm_ops()]
+        for j in range(4):
+            valu += [(op, xs + 2, z3 + 16 * j - 1) for op in softmax0_j(b0, j)]
+        # tile 1's mask and its keys 0-15, once P(rg, 0) has been read by
+        # tile 0's hi MFMAs of step 0
+        late = z3 + 16 + 4
+        valu += [("s_mov_b32 %[j0], 64", late, end)]
+        valu += [(op, late, end) for op in mask_ops(b1)]
+        valu += [(op, late, end) for op in softmax_j(b1, 0)]
+        # tile 1's first V fragments, once slots 0-3 (fragments 8-11 of
+        # tile 0) have been read by their last MFMAs
+        side += [(v_read(st1, nv), z3 + 3 * 16 + 2) for nv in range(4)]
+    run_slots(b, mfmas, reads, valu, side, first_use)
     return b.lines
 
 
@@ -390,14 +568,26 @@ def loop_text():
     L += ["v_mov_b32 v180, 0xff800000",
           "v_add_u32 v183, 0x10000, v181", "v_add_u32 v184, 0x10000, v182",
           "v_add_u32 v186, 0x10000, v185"]
-    L += ["s_mov_b32 %[j0], 64", "s_cmp_ge_u32 %[j0], %[tmask]", "s_cbranch_scc1 60f"]
-    L += fill(False)
-    L += ["s_branch 61f", "60:"]
-    L += fill(True)
-    L += ["61:", "s_mov_b32 %[t], 1"]
-    # dispatch on the last tile, t % 4 and the mask of tile t + 1
+    # the head: dispatch on tile 0's stage and on a single-tile item
+    L += ["s_and_b32 %[b0], %[tbase], 3", "s_add_u32 %[t], %[tbase], 1",
+          "s_cmp_ge_u32 %[t], %[tend]", "s_cbranch_scc1 48f"]
+    for stage in range(4):
+        L += [f"s_cmp_eq_u32 %[b0], {stage}", f"s_cbranch_scc1 {40 + stage}f"]
+    L += ["48:"]
+    for stage in range(4):
+        L += [f"s_cmp_eq_u32 %[b0], {stage}", f"s_cbranch_scc1 {44 + stage}f"]
+    for single in (False, True):
+        for stage in range(4):
+            L += [f"{40 + 4 * single + stage}:"]
+            L += head(stage, single)
+            if single:
+                L += ["s_branch 99f"]
+            else:
+                L += ["s_add_u32 %[t], %[tbase], 1", "s_branch 70f"]
+    # dispatch on the last tile, t % 4 and the mask of tile t + 1 (key
+    # index j0 = 64 (t + 1 - tbase))
     L += ["70:", "s_add_u32 %[j0], %[t], 1", "s_cmp_ge_u32 %[j0], %[tend]", "s_cbranch_scc1 71f",
-          "s_lshl_b32 %[j0], %[j0], 6", "s_and_b32 %[b0], %[t], 3"]
+          "s_sub_u32 %[j0], %[j0], %[tbase]", "s_lshl_b32 %[j0], %[j0], 6", "s_and_b32 %[b0], %[t], 3"]
     for stage in range(4):
         L += [f"s_cmp_eq_u32 %[b0], {stage}", f"s_cbranch_scc1 {80 + stage}f"]
     for stage in range(4):
@@ -429,8 +619,8 @@ def main():
     for l in lines:
         print(f'    "{l}\\n" \\')
     print('    ""')
-    clob = ([f'"v{i}"' for i in range(0, 164)] +
-            ['"v180"', '"v183"', '"v184"', '"v186"', '"v192"'] +
+    clob = ([f'"v{i}"' for i in range(0, 166)] +
+            ['"v180"', '"v183"', '"v184"', '"v186"', '"v192"', '"v193"'] +
             [f'"a{i}"' for i in range(192, 256)])
     print("#define VO_PREFILL_PIPE_CLOBBERS " + ", ".join(clob))
 

@@ -224,6 +224,13 @@ struct PrefillPlan {
     // the item's own rows, so a sequence's result does not depend on the
     // other sequences of the batch.
     uint32_t num_long = 0;
+    // The pipelined kernel's plan for items num_long .. num_items - 1, dealt
+    // to persistent workgroup slots: pipe[0 .. pipe_slots] are the slots'
+    // first descriptors, then [num_items - num_long][4] descriptors (first
+    // row, rows, position of first row, offset of the sequence's block
+    // table) ordered by slot.
+    const uint32_t *pipe = nullptr;
+    uint32_t pipe_slots = 0;
 };
 
 // Keys the DMA prefill kernel takes per row (its block table lives in LDS).

@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <queue>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -704,6 +705,21 @@ vo_status plan_decode(vo_step_meta *m, Packer &pk) { return plan_decode_rows(m, 
 // shapes, and each row is written by exactly one of them.  Items with rows
 // past prefill_dma_max_keys() keys (a multiple of 64, so exactly the items of
 // more tiles than that / 64) lead the order and are counted in num_long.
+// Per-item cost of the pipelined prefill kernel's slot plan, in KV tiles
+// (measured: an item's tile 0, overflow check, output and hand-over take
+// about five tiles' time).
+constexpr uint64_t kPipeItemCost = 5;
+
+// Persistent slots per KV head for the pipelined prefill kernel: the CUs'
+// share of one KV head (one workgroup fills a CU), at most one per item.
+// VO_PREFILL_PIPE_SLOTS=n sets the count (tests: long item chains per slot).
+uint32_t pipe_slot_count(const vo_step_meta *m, uint64_t items) {
+    uint64_t s = (m->num_cus && m->kv_heads) ? m->num_cus / m->kv_heads : 1;
+    const int forced = env_int("VO_PREFILL_PIPE_SLOTS", 0);
+    if (forced > 0) s = static_cast<uint64_t>(forced);
+    return static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(s, items)));
+}
+
 vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens,
                        const uint64_t *seq_row_starts) {
     m->prefill_planned = false;
@@ -757,6 +773,46 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
     }
     m->prefill_plan.max_keys = max_keys;
     m->prefill_plan.num_long = num_long;
+    // The pipelined kernel's persistent slots (one workgroup per slot and
+    // KV head): its items, longest first, each to the slot with the least
+    // work so far, counted in KV tiles plus kPipeItemCost per item (its
+    // tile 0 and the hand-over between items); ties go to the lower slot.
+    // Which slot runs an item changes no bit of its rows.
+    m->prefill_plan.pipe = nullptr;
+    m->prefill_plan.pipe_slots = 0;
+    const uint64_t n_pipe = items.size() - num_long;
+    if (n_pipe > 0) {
+        const uint32_t S = pipe_slot_count(m, n_pipe);
+        std::vector<uint32_t> slot_of(items.size()), count(S, 0);
+        using Load = std::pair<uint64_t, uint32_t>;
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (uint32_t s = 0; s < S; ++s) heap.push({0, s});
+        for (size_t k = num_long; k < items.size(); ++k) {
+            const Load top = heap.top();
+            heap.pop();
+            slot_of[k] = top.second;
+            ++count[top.second];
+            heap.push({top.first + items[k].tiles + kPipeItemCost, top.second});
+        }
+        const uint32_t *pp;
+        uint32_t *pw = pk.add(kRegPrefillPipe, S + 1 + 4 * n_pipe, &pp);
+        std::vector<uint32_t> at(S);
+        uint32_t sum = 0;
+        for (uint32_t s = 0; s < S; ++s) {
+            pw[s] = at[s] = sum;
+            sum += count[s];
+        }
+        pw[S] = sum;
+        for (size_t k = num_long; k < items.size(); ++k) {
+            uint32_t *d = pw + S + 1 + 4 * static_cast<uint64_t>(at[slot_of[k]]++);
+            d[0] = items[k].row;
+            d[1] = items[k].rows;
+            d[2] = items[k].pos;
+            d[3] = static_cast<uint32_t>(m->table_off[items[k].seq]);
+        }
+        m->prefill_plan.pipe = pp;
+        m->prefill_plan.pipe_slots = S;
+    }
     if (!m->decode_rows.empty())
         if (vo_status rc = plan_decode_rows(m, pk, &m->decode_rows)) return rc;
     m->prefill_planned = true;
@@ -849,6 +905,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
                           + max_rows                                         // positions
                           + 4 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
+                          + 5 * (max_rows + max_seqs) + 1                    // its slot plan
                           + max_seqs                                         // last rows
                           + (decode_pack_limit(m) - 1) * m->max_parts        // row-packing mates
                           + 10 * 64;                                         // alignment slack
@@ -1100,7 +1157,7 @@ extern "C" int32_t vo_step_meta_fix_launch(vo_step_meta *m, uint64_t work_headro
     const uint64_t S = f.seqs;
     const uint64_t caps[kNumRegions] = {
         2, S + 1, f.entries_cap, S, S, f.has_positions ? S : 0, S, 3 * S,
-        4 * f.work_cap, 2 * S, S, S, 0, 0};
+        4 * f.work_cap, 2 * S, S, S, 0, 0, 0};
     uint64_t off = 0;
     for (int r = 0; r < kNumRegions; ++r) {
         off = align_up(off, 256);

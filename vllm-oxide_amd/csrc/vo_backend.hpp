@@ -75,6 +75,7 @@ enum Region {
     kRegReduceRows,
     kRegLastRows,
     kRegPrefillWork,
+    kRegPrefillPipe,
     kRegMates,
     kNumRegions
 };
