@@ -843,7 +843,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
     const uint32_t kvh = blockIdx.x % kv_heads;
     const uint32_t slot = blockIdx.x / kv_heads;
-    const uint32_t *descs = plan + num_slots + 1;
+    // The slot's first record (its first item's descriptor, that item's
+    // tiles 0-2 block ids, the next item's first twelve) sits at an address
+    // that depends only on the slot, so the first DMAs, Q loads and table
+    // copy wait for one load.
+    const uint32_t *first = plan + num_slots + 1 + kPipeFirstWords * slot;
+    const uint32_t *descs = plan + num_slots + 1 + kPipeFirstWords * num_slots;
     uint32_t i = plan[slot];
     const uint32_t i_end = plan[slot + 1];
     if (i >= i_end) return;  // the host plan gives every slot an item
@@ -887,9 +892,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const uint32_t st0 = lds_addr(st);
     const uint32_t wbase = st0 + 1024 * head;
 
-    PipeItem A = pipe_item(descs + 4 * i, tables);
+    // The current item, the next (its first block ids go into the current
+    // item's table) and the one after (loaded a hand-over ahead of its use).
+    PipeItem A = pipe_item(first, tables);
     bool has_b = i + 1 < i_end;
     PipeItem B = pipe_item(descs + 4 * (has_b ? i + 1 : i), tables);
+    bool has_c = i + 2 < i_end;
+    PipeItem C = pipe_item(descs + 4 * (has_c ? i + 2 : i), tables);
     uint32_t T = 0;  // stage of the current item's tile 0
 
     // LDS DMA of a tile with block byte offsets b into `stage`.
@@ -916,12 +925,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int k = 0; k < 4; ++k) b[k] = uniform_u32(tbl[4 * t + k]) * stride;
         dma_raw((T + t) % 4, b);
     };
-    // The same with the ids read from the item's table in global memory
-    // (scalar loads, clamped to its last block), before the LDS copy exists.
-    auto dma_global = [&](const PipeItem &it, uint32_t t) __attribute__((always_inline)) {
+    // The first item's tile t (0-2) with the ids from the slot's record,
+    // before the LDS copy exists.
+    auto dma_first = [&](uint32_t t) __attribute__((always_inline)) {
         uint32_t b[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) b[k] = uniform_u32(it.table[min(4 * t + k, it.nblk - 1)]) * stride;
+        for (int k = 0; k < 4; ++k) b[k] = uniform_u32(first[4 + 4 * t + k]) * stride;
         dma_raw((T + t) % 4, b);
     };
     // The item's block ids into the LDS table, then the next item's first
@@ -950,19 +959,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
     };
 
-    // The first item: its first three tiles' DMA goes out first, so that
-    // its latency, the table copy's and Q's overlap behind one wait.
+    // The first item: its first three tiles' DMA goes out first, then Q,
+    // then the table copy, so that their latencies overlap behind one wait.
     if (fixed_offset) {
-        dma_global(A, 0);
-        dma_global(A, 1);
-        dma_global(A, 2);
+        dma_first(0);
+        dma_first(1);
+        dma_first(2);
     }
-    copy_table(A, has_b, B);
+    load_q(A);
+    {
+        // the first item's ids, then the next item's first twelve from the
+        // record (the entries after them are never used for a DMA)
+        const uint32_t n4 = 4 * A.n_tiles;
+        const uint32_t ntbl = min(n4 + 16, static_cast<uint32_t>(kTableLds + 16));
+        for (uint32_t k = ln.tid; k < ntbl; k += 256)
+            tbl[k] = k < n4 ? A.table[min(k, A.nblk - 1)] : first[16 + min(k - n4, 11u)];
+    }
     if (ln.tid == 0) {
         redo[0] = 0u;
         redo[1] = 0u;
     }
-    load_q(A);
     wait_barrier<0>();  // the table copy, Q and (fixed offset) tiles 0-2
     // Tiles 0-2 of the current item are in their stages (issued and waited
     // for, or in flight from the previous item's DMAs past its end).
@@ -1171,13 +1187,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         }
 
         // The next item's Q (this item's is no longer needed).
-        bool has_c = false;
-        PipeItem C = B;
-        if (has_b) {
-            load_q(B);
-            has_c = i + 2 < i_end;
-            C = pipe_item(descs + 4 * (has_c ? i + 2 : i + 1), tables);
-        }
+        if (has_b) load_q(B);
 
         // Output: each wave its own head's rows, one row group at a time,
         // through 8 KiB of the stage that holds no prefetched tile (this
@@ -1208,12 +1218,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 uint16_t *obase = out + (static_cast<uint64_t>(A.row_begin + kRG * rg) * num_heads + qhead) * HD;
+                // every chunk read first (one wait), then the stores of the
+                // item's rows
+                constexpr int NK = kRG * CH / 64;
+                u32x4 vals[NK];
 #pragma unroll
-                for (int k = 0; k < kRG * CH / 64; ++k) {
-                    const uint32_t idx = ln.lane + 64 * k;
-                    const uint32_t row = idx / CH;
-                    const uint32_t q4 = idx % CH;
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(wst + row * ROWB + 16 * (q4 ^ (row % CH)));
+                for (int k = 0; k < NK; ++k) {
+                    const uint32_t row = (ln.lane + 64 * k) / CH;
+                    const uint32_t q4 = ln.lane % CH;
+                    vals[k] = *reinterpret_cast<const u32x4 *>(wst + row * ROWB + 16 * (q4 ^ (row % CH)));
+                }
+#pragma unroll
+                for (int k = 0; k < NK; ++k) {
+                    const uint32_t row = (ln.lane + 64 * k) / CH;
+                    const uint32_t q4 = ln.lane % CH;
+                    const u32x4 v = vals[k];
                     if (kRG * rg + row < A.nrows)
                         __builtin_nontemporal_store(
                             v, reinterpret_cast<u32x4 *>(obase + static_cast<uint64_t>(row) * num_heads * HD + 8 * q4));
@@ -1230,12 +1249,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // rewrites that stage.
         copy_table(B, has_c, C);
         T = (T + n_tiles) % 4;
-        wait_barrier<0>();
         ready = next_ready;
         A = B;
         B = C;
         has_b = has_c;
         ++i;
+        has_c = i + 2 < i_end;
+        C = pipe_item(descs + 4 * (has_c ? i + 2 : i), tables);  // waited for by the barrier
+        wait_barrier<0>();
     }
     // The last item's DMAs past its end write LDS: they land before the
     // workgroup ends.

@@ -72,6 +72,11 @@ BT = 4096  # bytes of one (block, KV head) tile at head_dim 128
 
 K_AHEAD = 8   # MFMA slots between a K fragment's read and its first use
 V_AHEAD = 7   # the same for V fragments
+DMA_SPREAD = 4  # MFMA slots between the tile DMA's eight loads (the last
+                # tile's iteration: half).  Each buffer load with a VGPR
+                # address costs about 20 cycles of MFMA issue on gfx950; the
+                # four wavefronts issue theirs at the same slots, and spread
+                # out they overlap the running MFMAs better (-1 to -2%).
 
 
 def O(rg, dt):
@@ -350,13 +355,17 @@ def iteration(stage, masked_next, last):
     if not last:
         reads += [(("k", n), k_read(kst, n), K_AHEAD) for n in range(16)]
     reads += [(("v", nv), v_read(stage, nv), V_AHEAD) for nv in range(4, 16)]
-    side = [(op, 0) for op in dma_side((stage + 3) % 4)]
+    dops = dma_side((stage + 3) % 4)
+    side = [(op, 0) for op in dops[:8]]
+    spread = DMA_SPREAD if not last else DMA_SPREAD // 2
+    side += [(op, spread * (i // 3)) for i, op in enumerate(dops[8:])]
     if not last:
         side += [("ds_read_b128 v[160:163], v189", 1), ("v_add_u32 v189, 16, v189", 1)]
         # the next tile's first V fragments, once slots 0-3 (fragments
         # 8-11 of this tile) have been read by their MFMAs
         pre = first_use[("v", 11)] + 2
         side += [(v_read(kst, nv), pre) for nv in range(4)]
+    side.sort(key=lambda e: e[1])
     valu = []
     for j in (1, 2, 3):
         valu += [(op, 0, first_use[("v", 4 * j)] - 1) for op in softmax_j(cur, j)]
@@ -367,33 +376,6 @@ def iteration(stage, masked_next, last):
         valu += [(op, ready, end) for op in softmax_j(nxt, 0)]
     run_slots(b, mfmas, reads, valu, side, first_use)
     return b.lines
-
-
-def fill(stage, masked):
-    """Before iteration 1, tile 1 in `stage`: tile 1 has landed (vmcnt(16):
-    tiles 2 and 3 in flight); ids of tile 4; Q.K^T of tile 1 into S buffer
-    stage % 2, its mask if needed, P of its keys 0-15, and its first V
-    fragments."""
-    buf = stage % 2
-    b = Body()
-    b.emit("s_waitcnt vmcnt(16) lgkmcnt(0)")
-    b.emit("s_barrier")
-    mfmas, first_use = [], {}
-    for n in range(16):
-        for rg in range(2):
-            first_use.setdefault(("k", n), len(mfmas))
-            mfmas.append((qk_mfma(buf, n, rg), ("k", n), []))
-    reads = [(("k", n), k_read(stage, n), K_AHEAD) for n in range(16)]
-    side = [("ds_read_b128 v[160:163], v189", 0), ("v_add_u32 v189, 16, v189", 0)]
-    run_slots(b, mfmas, reads, [], side, first_use)
-    b.lines += ["s_nop 7", "s_nop 7", "s_nop 7"]
-    if masked:
-        b.lines += mask_ops(buf)
-    b.lines += softmax_j(buf, 0)
-    for nv in range(4):
-        b.lds(v_read(stage, nv))
-    return b.lines
-
 
 
 def max_ops(buf):

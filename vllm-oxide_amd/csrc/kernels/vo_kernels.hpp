@@ -212,6 +212,8 @@ hipError_t launch_decode_mfma(const PoolLayer &pool, const MetaView &meta,
                               uint32_t num_heads, float scale, int waves_per_group,
                               hipStream_t stream, const NewKeys *new_keys = nullptr);
 
+constexpr uint32_t kPipeFirstWords = 28;
+
 // Work plan of the MFMA prefill kernel: one item per 32-row query tile of a
 // sequence, longest first.
 struct PrefillPlan {
@@ -226,9 +228,11 @@ struct PrefillPlan {
     uint32_t num_long = 0;
     // The pipelined kernel's plan for items num_long .. num_items - 1, dealt
     // to persistent workgroup slots: pipe[0 .. pipe_slots] are the slots'
-    // first descriptors, then [num_items - num_long][4] descriptors (first
-    // row, rows, position of first row, offset of the sequence's block
-    // table) ordered by slot.
+    // first descriptor indices, then each slot's first record
+    // (kPipeFirstWords words: its first item's descriptor, the block ids of
+    // that item's tiles 0-2 and the next item's first twelve), then
+    // [num_items - num_long][4] descriptors (first row, rows, position of
+    // first row, offset of the sequence's block table) ordered by slot.
     const uint32_t *pipe = nullptr;
     uint32_t pipe_slots = 0;
 };

@@ -795,7 +795,8 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
             heap.push({top.first + items[k].tiles + kPipeItemCost, top.second});
         }
         const uint32_t *pp;
-        uint32_t *pw = pk.add(kRegPrefillPipe, S + 1 + 4 * n_pipe, &pp);
+        uint32_t *pw = pk.add(kRegPrefillPipe,
+                              S + 1 + kernels::kPipeFirstWords * S + 4 * n_pipe, &pp);
         std::vector<uint32_t> at(S);
         uint32_t sum = 0;
         for (uint32_t s = 0; s < S; ++s) {
@@ -803,12 +804,31 @@ vo_status plan_prefill(vo_step_meta *m, Packer &pk, const uint64_t *context_lens
             sum += count[s];
         }
         pw[S] = sum;
+        uint32_t *const descs = pw + S + 1 + kernels::kPipeFirstWords * S;
         for (size_t k = num_long; k < items.size(); ++k) {
-            uint32_t *d = pw + S + 1 + 4 * static_cast<uint64_t>(at[slot_of[k]]++);
+            uint32_t *d = descs + 4 * static_cast<uint64_t>(at[slot_of[k]]++);
             d[0] = items[k].row;
             d[1] = items[k].rows;
             d[2] = items[k].pos;
             d[3] = static_cast<uint32_t>(m->table_off[items[k].seq]);
+        }
+        // Each slot's first record: its first item's descriptor, the block
+        // ids of that item's tiles 0-2, and the next item's first twelve
+        // (copies of the item's last id when the slot has one item), each
+        // clamped to the item's last block -- what the kernel's first DMAs
+        // and block table need, at an address that depends only on the slot.
+        // (nblk at the step's block size: the rows' checked table coverage)
+        auto block_id = [&](const uint32_t *d, uint32_t k) {
+            const uint64_t nblk = (static_cast<uint64_t>(d[2]) + d[1] - 1) / m->block_size + 1;
+            return m->tables[d[3] + std::min<uint64_t>(k, nblk - 1)];
+        };
+        for (uint32_t s = 0; s < S; ++s) {
+            uint32_t *f = pw + S + 1 + kernels::kPipeFirstWords * static_cast<uint64_t>(s);
+            const uint32_t *d0 = descs + 4 * static_cast<uint64_t>(pw[s]);
+            const uint32_t *d1 = count[s] > 1 ? d0 + 4 : nullptr;
+            for (int w = 0; w < 4; ++w) f[w] = d0[w];
+            for (uint32_t k = 0; k < 12; ++k) f[4 + k] = block_id(d0, k);
+            for (uint32_t k = 0; k < 12; ++k) f[16 + k] = d1 ? block_id(d1, k) : block_id(d0, 0xffffffffu);
         }
         m->prefill_plan.pipe = pp;
         m->prefill_plan.pipe_slots = S;
@@ -905,7 +925,7 @@ extern "C" int32_t vo_step_meta_create(const vo_kv_pool *pool, uint64_t max_seqs
                           + max_rows                                         // positions
                           + 4 * m->max_parts + 3 * max_rows                  // decode plan
                           + 4 * (max_rows + max_seqs)                        // prefill plan
-                          + 5 * (max_rows + max_seqs) + 1                    // its slot plan
+                          + (5 + kernels::kPipeFirstWords) * (max_rows + max_seqs) + 1  // its slot plan
                           + max_seqs                                         // last rows
                           + (decode_pack_limit(m) - 1) * m->max_parts        // row-packing mates
                           + 10 * 64;                                         // alignment slack
