@@ -768,13 +768,15 @@ __global__ __launch_bounds__(64 * G * R) __attribute__((amdgpu_waves_per_eu(
 //
 // Four LDS stages (the tile in P.V, the tile in Q.K^T, and two in flight):
 // the DMA of tile t + 3 is issued at iteration t, after a barrier that
-// follows the wait for tile t + 1.  Tile 0 (whose max becomes the fixed
-// softmax offset and whose P goes in as bf16 hi + lo), the masked tiles at
-// the diagonal and the running-max recompute run as ordinary code.  Per row
-// the arithmetic is the 32-row kernels' operation for operation (same
-// MFMAs in the same order from the same LDS bytes, same VALU operations),
-// so a row gets the same bits here as in prefill_dma_kernel<128, 4, 1>,
-// which serves the same items on small grids.
+// follows the wait for tile t + 1.  The generated code also runs tile 0
+// (whose max becomes the fixed softmax offset and whose P goes in as bf16
+// hi + lo) and the causal masks; the overflow check, the running-max
+// recompute and the output run as ordinary code between items.  Per row the
+// arithmetic is the 32-row kernels' operation for operation (same MFMAs in
+// the same order from the same LDS bytes, same VALU operations), so a row
+// gets the same bits here as in prefill_dma_kernel<128, 4, 1>, which serves
+// the same items on small grids.  The kernel is persistent (below): one
+// workgroup per CU runs a slot's items through one LDS ring.
 #include "prefill_pipe_loop.inc"
 
 // The four words of a raw buffer resource, for an inline-asm operand.
