@@ -1085,9 +1085,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // is off).  Its tiles 0-2 are issued here; the caller has waited for
         // every DMA in flight.
         auto plain_pass = [&](auto running_c, const bool (&live)[2]) __attribute__((always_inline)) {
+            // every group's state starts over (a group not in `live` keeps
+            // zeros, unused), so nothing of the first pass stays live here
 #pragma unroll
             for (int rg = 0; rg < 2; ++rg) {
-                if (!live[rg]) continue;
                 m_run[rg] = 0.0f;
                 l_run[rg] = 0.0f;
 #pragma unroll
@@ -1109,6 +1110,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int rg = 0; rg < 2; ++rg)
                 if (live[rg]) l_run[rg] += __shfl_xor(l_run[rg], 32, 64);
+        };
+
+        // A row group's output as bf16, O scaled by 1 / l, made as soon as
+        // the group's pass ends: the accumulators are read once and are dead
+        // across the barrier and the output that follow.
+        bf16x4 packed[2][DT][4];
+        auto pack_out = [&](int rg) __attribute__((always_inline)) {
+            const float inv = 1.0f / l_run[rg];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        packed[rg][dt][r4][e] = static_cast<__bf16>(o_acc[rg][dt][4 * r4 + e] * inv);
         };
 
         // Tiles nA .. nA + 2 of this item's ring positions carry the next
@@ -1171,79 +1187,96 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 const bool ok = l_run[rg] < kOverflowSum && all_finite(o_acc[rg]);  // false for inf, NaN
                 if (__builtin_amdgcn_ballot_w64(kRG * rg + ln.c < A.nrows && !ok) != 0 && ln.lane == 0)
                     atomicOr(my_redo, 1u << rg);
+                pack_out(rg);
             }
-        } else if (ln.tid == 0) {
-            *my_redo = 3u;
+        } else {
+            // every row group runs in the pass below, which packs it
+            if (ln.tid == 0) *my_redo = 3u;
         }
+        // Output of one row group: each wave its own head's rows, through
+        // 8 KiB of the stage that holds no prefetched tile (this item's last
+        // tile's); chunk q of row c at q ^ (c % 16).  The stores are
+        // non-temporal: the output is not read again by this kernel, and
+        // lines left dirty in L2 are written back when the kernel ends.
+        auto write_out = [&](int rg) __attribute__((always_inline)) {
+            constexpr int ROWB = HD * 2;
+            constexpr int CH = HD / 8;
+            uint8_t *wst = st + ((T + n_tiles + 3) % 4) * kPipeStage + head * (kRG * ROWB);
+            uint8_t *row_at = wst + ln.c * ROWB + 8 * ln.gl;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const uint32_t q4 = static_cast<uint32_t>(4 * dt + r4) ^ (ln.c % CH);
+                    *reinterpret_cast<bf16x4 *>(row_at + 16 * q4) = packed[rg][dt][r4];
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            uint8_t *obase = reinterpret_cast<uint8_t *>(
+                out + (static_cast<uint64_t>(A.row_begin + kRG * rg) * num_heads + qhead) * HD);
+            // every chunk read first (one wait), then the stores of the
+            // item's rows; lane L stores chunk L % 16 of rows L / 16 + 4 k
+            constexpr int NK = kRG * CH / 64;
+            const uint32_t row_bytes = num_heads * HD * 2;
+            const uint32_t row0 = ln.lane / CH;
+            const uint32_t q4 = ln.lane % CH;
+            const uint32_t voff = row0 * row_bytes + 16 * q4;
+            u32x4 vals[NK];
+#pragma unroll
+            for (int k = 0; k < NK; ++k) {
+                const uint32_t row = row0 + (64 / CH) * k;
+                vals[k] = *reinterpret_cast<const u32x4 *>(wst + row * ROWB + 16 * (q4 ^ (row % CH)));
+            }
+#pragma unroll
+            for (int k = 0; k < NK; ++k) {
+                const uint32_t row = row0 + (64 / CH) * k;
+                if (kRG * rg + row < A.nrows)
+                    __builtin_nontemporal_store(
+                        vals[k], reinterpret_cast<u32x4 *>(obase + (voff + (64 / CH) * k * row_bytes)));
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        };
+
         wait_barrier<63>();  // the flags; every wave is done with this item's tiles
         const uint32_t again = uniform_u32(*my_redo);
         if (again != 0) {
             // The recompute with the running max for the 32-row groups that
             // left the fixed-offset range (prefill_dma_kernel's second pass),
             // after the DMAs in flight (the next item's tiles) have landed.
+            // A group kept from the first pass is written first, so that no
+            // packed output is held across the pass.
             const bool live[2] = {(again & 1u) != 0, (again & 2u) != 0};
-            wait_barrier<0>();
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg)
+                if (!live[rg]) write_out(rg);
+            wait_barrier<0>();  // also every wave's staging reads, before the DMA rewrites the stages
             plain_pass(True{}, live);
             next_ready = true;
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg) {
+                if (live[rg]) {
+                    pack_out(rg);
+                } else {
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) packed[rg][dt][r4] = bf16x4{};  // written above
+                }
+            }
             wait_barrier<63>();  // every wave is done with the stages
         }
 
         // The next item's Q (this item's is no longer needed).
         if (has_b) load_q(B);
 
-        // Output: each wave its own head's rows, one row group at a time,
-        // through 8 KiB of the stage that holds no prefetched tile (this
-        // item's last tile's); chunk q of row c at q ^ (c % 16).  The stores
-        // are non-temporal: the output is not read again by this kernel, and
-        // lines left dirty in L2 are written back when the kernel ends.
-        {
-            constexpr int ROWB = HD * 2;
-            constexpr int CH = HD / 8;
-            uint8_t *wst = st + ((T + n_tiles + 3) % 4) * kPipeStage + head * (kRG * ROWB);
+        // The row groups not written above, one at a time.
 #pragma unroll
-            for (int rg = 0; rg < 2; ++rg) {
-                const float inv = 1.0f / l_run[rg];
-                uint8_t *row_at = wst + ln.c * ROWB + 8 * ln.gl;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-                    for (int r4 = 0; r4 < 4; ++r4) {
-                        bf16x4 packed;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            packed[e] = static_cast<__bf16>(o_acc[rg][dt][4 * r4 + e] * inv);
-                        const uint32_t q4 = static_cast<uint32_t>(4 * dt + r4) ^ (ln.c % CH);
-                        *reinterpret_cast<bf16x4 *>(row_at + 16 * q4) = packed;
-                    }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                uint16_t *obase = out + (static_cast<uint64_t>(A.row_begin + kRG * rg) * num_heads + qhead) * HD;
-                // every chunk read first (one wait), then the stores of the
-                // item's rows
-                constexpr int NK = kRG * CH / 64;
-                u32x4 vals[NK];
-#pragma unroll
-                for (int k = 0; k < NK; ++k) {
-                    const uint32_t row = (ln.lane + 64 * k) / CH;
-                    const uint32_t q4 = ln.lane % CH;
-                    vals[k] = *reinterpret_cast<const u32x4 *>(wst + row * ROWB + 16 * (q4 ^ (row % CH)));
-                }
-#pragma unroll
-                for (int k = 0; k < NK; ++k) {
-                    const uint32_t row = (ln.lane + 64 * k) / CH;
-                    const uint32_t q4 = ln.lane % CH;
-                    const u32x4 v = vals[k];
-                    if (kRG * rg + row < A.nrows)
-                        __builtin_nontemporal_store(
-                            v, reinterpret_cast<u32x4 *>(obase + static_cast<uint64_t>(row) * num_heads * HD + 8 * q4));
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            }
-        }
+        for (int rg = 0; rg < 2; ++rg)
+            if (again == 0 || ((again >> rg) & 1u) != 0) write_out(rg);
         if (!has_b) break;
         // The next item: its table (and the first ids of the one after),
         // then one wait for its Q, its table and its tiles 0-2; the barrier
