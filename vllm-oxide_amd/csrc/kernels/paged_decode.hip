@@ -562,6 +562,10 @@ __device__ __forceinline__ void shared_split_pairs(
     // lanes of floatx4 per state (one stage), and (m, l) per state and lane.
     static_assert(2 * DT * 64 * 16 <= S::BYTES && kTiles * 4 * 64 * 4 <= S::BYTES,
                   "pair exchange fits the stages");
+    // The packs set the launch's length and share each CU with a
+    // register-path workgroup that has slack: their wavefronts win the
+    // SIMDs' issue arbitration.
+    __builtin_amdgcn_s_setprio(3);
 
     const uint32_t row = uniform_u32(rec[0]);
     const uint32_t split = uniform_u32(rec[1]);
