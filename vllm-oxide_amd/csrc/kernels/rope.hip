@@ -13,14 +13,16 @@
 // rope_rows_kernel: one thread per (row, head, 8 pairs), or per pair when
 // half is not a multiple of 8; 16-byte loads and stores in the first case.
 // rope_cache_kernel: the layer's "rope(q); rope(k); write_kv(k, v)"
-// (model.rs:307-311) as one launch over the step's write plan: one wavefront
-// per (run of rows with consecutive slots in one block, KV head).  A lane
-// owns 8 dims of a row; its rotation partner (the other half of the head) is
-// the lane UPR/2 away in the same row, reached with a lane shuffle.  The
-// wavefront rotates the run's q rows for the G query heads of its KV head in
-// place, writes the rotated K into the key-major tile and V into the
-// dim-major tile (transposed in registers, 32-byte runs per dim for a whole
-// block), reading each row's cos/sin once.  q may be read from one buffer
+// (model.rs:307-311) as one launch over the step's write plan: one workgroup
+// per (run of rows with consecutive slots in one block, KV head), and in it
+// one wavefront per RPI rows of the run (4 at head_dim 128), so that each
+// wavefront waits for one chain of loads.  A lane owns 8 dims of a row; its
+// rotation partner (the other half of the head) is the lane UPR/2 away in
+// the same row, reached with a lane shuffle.  The wavefront rotates its rows'
+// q for the G query heads of its KV head in place, writes the rotated K into
+// the key-major tile and V into the dim-major tile (transposed in registers:
+// per dim the wavefront's RPI keys, 2 RPI bytes, in a whole block's run),
+// reading each row's cos/sin once.  q may be read from one buffer
 // and written to another (the rows of a fused QKV projection output are
 // strided: q_in_ld, kv_ld), or rotated in place (q_in == q_out).
 //
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(uint16_t *__restrict__ x
 }
 
 template <int HD>
-__global__ __launch_bounds__(256) void rope_cache_kernel(
+__global__ __launch_bounds__(64 * (16 / (64 / (HD / 8)))) void rope_cache_kernel(
     uint16_t *__restrict__ k_pool, uint16_t *__restrict__ v_pool, uint32_t kv_heads,
     const uint16_t *q_in, uint32_t q_in_ld, uint16_t *q_out, uint32_t q_out_ld, uint32_t group,
     const uint16_t *__restrict__ keys, const uint16_t *__restrict__ values, uint32_t kv_ld,
@@ -119,27 +121,50 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
     constexpr uint32_t HALF = HD / 2;
     constexpr int DPL = HD / 64;        // V dims per lane
     constexpr uint32_t UPR = HD / 8;    // 16-byte units per row of one head
-    constexpr uint32_t RPI = 64 / UPR;  // rows per instruction
-    constexpr uint32_t KI = BS / RPI;
-    const uint32_t item = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= num_items) return;  // whole wavefront
+    constexpr uint32_t RPI = 64 / UPR;  // rows per pass (one instruction covers them)
+    // One workgroup per (run, KV head); wavefront w takes the run's rows
+    // RPI w .. RPI w + RPI - 1, so a wavefront's loads form one dependent
+    // chain (position, then cos/sin, K, Q) instead of one per pass.
+    const uint32_t item = blockIdx.x;
+    if (item >= num_items) return;
+    const uint32_t pass = threadIdx.x >> 6;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t seg = item / kv_heads;
     const uint32_t kvh = item % kv_heads;
     const uint32_t row0 = segments[3 * seg];
     const uint32_t n = segments[3 * seg + 1];  // 1 .. BS
     const uint32_t slot0 = segments[3 * seg + 2];
+    if (RPI * pass >= n) return;  // whole wavefront: no row of the run in this pass
     // A superseded row (slot kSkipSlot) only has its q rotated.
     const bool cache = slot0 != kSkipSlot;
     const uint32_t off0 = cache ? slot0 % BS : 0;
     const uint64_t width = kv_ld;
     const uint64_t tile = cache ? (static_cast<uint64_t>(slot0 / BS) * kv_heads + kvh) * (BS * HD) : 0;
 
+    // V of this pass's rows (dims DPL lane .. + DPL - 1), loaded first: it
+    // depends on nothing else.  Rows past the run load its last row (not
+    // stored), so the loads go out together, without a branch between them.
+    uint16_t vv[DPL][RPI];
+    {
+        const uint16_t *vsrc = values + static_cast<uint64_t>(row0) * width + kvh * HD + DPL * lane;
+#pragma unroll
+        for (uint32_t ii = 0; ii < RPI; ++ii) {
+            const uint32_t iv = min(RPI * pass + ii, n - 1);
+            if constexpr (DPL == 2) {
+                const uint32_t w = *reinterpret_cast<const uint32_t *>(vsrc + iv * width);
+                vv[0][ii] = static_cast<uint16_t>(w & 0xffffu);
+                vv[1][ii] = static_cast<uint16_t>(w >> 16);
+            } else {
+                vv[0][ii] = vsrc[iv * width];
+            }
+        }
+    }
+
     const uint32_t u = lane % UPR;
     const bool first_half = u < UPR / 2;
     const uint32_t d = 8 * u;
     const uint32_t p0 = 8 * (u % (UPR / 2));  // first pair of the lane's 8 dims
-    const uint32_t i0 = lane / UPR;
+    const uint32_t i = lane / UPR + RPI * pass;
 
     // Rotates a lane's 8 dims with its partner lane's (the other half).
     auto rot = [&](u32x4 own, const float *c, const float *s) -> u32x4 {
@@ -152,16 +177,26 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
         return first_half ? a : b;
     };
 
-#pragma unroll
-    for (uint32_t j = 0; j < KI; ++j) {
-        // Passes wholly past the run are skipped (n is the same for the whole
-        // wavefront); a one-row run of a decode step takes one pass.
-        if (RPI * j >= n) break;
-        const uint32_t i = i0 + RPI * j;
+    {
         // Every lane of a row takes part in the shuffles, so rows past the
         // run clamp to its last row and skip only the stores.
         const bool live = i < n;
         const uint32_t row = row0 + min(i, n - 1);
+        // K and the first four query heads need only the row: they load
+        // beside the position, before the cos/sin that wait for it.  Later
+        // heads (G > 4) load after the first ones' stores (q may be rotated
+        // in place).
+        const u32x4 kin = *reinterpret_cast<const u32x4 *>(keys + row * width + kvh * HD + d);
+        auto load_q4 = [&](uint32_t h0, u32x4 (&qin)[4]) {
+#pragma unroll
+            for (uint32_t hh = 0; hh < 4; ++hh) {
+                const uint32_t h = min(h0 + hh, group - 1);
+                const uint32_t col = (kvh * group + h) * HD + d;
+                qin[hh] = *reinterpret_cast<const u32x4 *>(q_in + static_cast<uint64_t>(row) * q_in_ld + col);
+            }
+        };
+        u32x4 qfirst[4];
+        load_q4(0, qfirst);
         const uint64_t t = static_cast<uint64_t>(positions[row]) * HALF + p0;
         float c[8], s[8];
 #pragma unroll
@@ -169,7 +204,6 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
             c[k] = cos_tab[t + k];
             s[k] = sin_tab[t + k];
         }
-        const u32x4 kin = *reinterpret_cast<const u32x4 *>(keys + row * width + kvh * HD + d);
         const u32x4 kout = rot(kin, c, s);
         if (live && cache)
             *reinterpret_cast<u32x4 *>(k_pool + tile + (d / 32) * (BS * 32) + (off0 + i) * 32 + d % 32) = kout;
@@ -177,11 +211,11 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
         // are in flight rather than one.
         for (uint32_t h0 = 0; h0 < group; h0 += 4) {
             u32x4 qin[4];
+            if (h0 == 0) {
 #pragma unroll
-            for (uint32_t hh = 0; hh < 4; ++hh) {
-                const uint32_t h = min(h0 + hh, group - 1);
-                const uint32_t col = (kvh * group + h) * HD + d;
-                qin[hh] = *reinterpret_cast<const u32x4 *>(q_in + static_cast<uint64_t>(row) * q_in_ld + col);
+                for (uint32_t hh = 0; hh < 4; ++hh) qin[hh] = qfirst[hh];
+            } else {
+                load_q4(h0, qin);
             }
 #pragma unroll
             for (uint32_t hh = 0; hh < 4; ++hh) {
@@ -194,40 +228,28 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(
     }
 
     if (!cache) return;
-    uint16_t vv[DPL][BS];
-    const uint16_t *vsrc = values + static_cast<uint64_t>(row0) * width + kvh * HD + DPL * lane;
-#pragma unroll
-    for (uint32_t i = 0; i < BS; ++i) {
-        if (i < n) {
-            if constexpr (DPL == 2) {
-                const uint32_t w = *reinterpret_cast<const uint32_t *>(vsrc + i * width);
-                vv[0][i] = static_cast<uint16_t>(w & 0xffffu);
-                vv[1][i] = static_cast<uint16_t>(w >> 16);
-            } else {
-                vv[0][i] = vsrc[i * width];
-            }
-        }
-    }
+    // This pass's RPI keys of each of the lane's dims in the dim-major V
+    // tile: one 2 RPI-byte store per dim for a whole run, else key by key.
     uint16_t *vdst = v_pool + tile + static_cast<uint64_t>(DPL * lane) * BS;
     if (n == BS) {
 #pragma unroll
         for (int e = 0; e < DPL; ++e) {
-            u32x4 lo, hi;
+            uint32_t w[RPI / 2];
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                lo[p] = static_cast<uint32_t>(vv[e][2 * p]) | (static_cast<uint32_t>(vv[e][2 * p + 1]) << 16);
-                hi[p] = static_cast<uint32_t>(vv[e][8 + 2 * p]) |
-                        (static_cast<uint32_t>(vv[e][8 + 2 * p + 1]) << 16);
-            }
-            *reinterpret_cast<u32x4 *>(vdst + e * BS) = lo;
-            *reinterpret_cast<u32x4 *>(vdst + e * BS + 8) = hi;
+            for (uint32_t p = 0; p < RPI / 2; ++p)
+                w[p] = static_cast<uint32_t>(vv[e][2 * p]) | (static_cast<uint32_t>(vv[e][2 * p + 1]) << 16);
+            if constexpr (RPI == 4)
+                *reinterpret_cast<u32x2 *>(vdst + e * BS + RPI * pass) = u32x2{w[0], w[1]};
+            else
+                *reinterpret_cast<u32x4 *>(vdst + e * BS + RPI * pass) = u32x4{w[0], w[1], w[2], w[3]};
         }
     } else {
 #pragma unroll
-        for (uint32_t i = 0; i < BS; ++i) {
-            if (i < n) {
+        for (uint32_t ii = 0; ii < RPI; ++ii) {
+            const uint32_t iv = RPI * pass + ii;
+            if (iv < n) {
 #pragma unroll
-                for (int e = 0; e < DPL; ++e) vdst[e * BS + off0 + i] = vv[e][i];
+                for (int e = 0; e < DPL; ++e) vdst[e * BS + off0 + iv] = vv[e][ii];
             }
         }
     }
@@ -262,16 +284,17 @@ hipError_t launch_rope_cache(const PoolLayer &pool, const uint16_t *q_in, uint32
     if (plan.num_segments == 0) return hipSuccess;
     if (!cache_write_supported(pool.head_dim, pool.block_size)) return hipErrorInvalidValue;
     const uint64_t items = static_cast<uint64_t>(plan.num_segments) * pool.kv_heads;
-    const uint64_t grid = (items + 3) / 4;
+    const uint64_t grid = items;  // one workgroup per (run, KV head)
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     KernelTimer timer("rope_cache", stream);
+    // block 16 rows: head_dim 128 takes 4 rows per pass (4 wavefronts), 64 takes 8 (2)
     if (pool.head_dim == 128)
         hipLaunchKernelGGL((rope_cache_kernel<128>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
                            stream, pool.k, pool.v, pool.kv_heads, q_in, q_in_ld, q_out, q_out_ld, group,
                            keys, values, kv_ld, plan.segments, positions, cos_tab, sin_tab,
                            static_cast<uint32_t>(items));
     else
-        hipLaunchKernelGGL((rope_cache_kernel<64>), dim3(static_cast<uint32_t>(grid)), dim3(256), 0,
+        hipLaunchKernelGGL((rope_cache_kernel<64>), dim3(static_cast<uint32_t>(grid)), dim3(128), 0,
                            stream, pool.k, pool.v, pool.kv_heads, q_in, q_in_ld, q_out, q_out_ld, group,
                            keys, values, kv_ld, plan.segments, positions, cos_tab, sin_tab,
                            static_cast<uint32_t>(items));
