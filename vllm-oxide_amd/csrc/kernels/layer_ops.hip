@@ -25,6 +25,7 @@ namespace kernels {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kNormRegIt = 4;  // rmsnorm rows up to kThreads * 8 * 4 columns stay in registers
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -104,8 +105,9 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(const uint32_t *_
 // Backend::rmsnorm (cpu/mod.rs:182-197): out = w * (x * (1 / sqrt(mean(x^2)
 // + eps))), the reference's (and HF's) order.  Row i of out normalises row
 // rows_idx[i] of x (the LM head's gather_rows, model.rs:334-340), or row i
-// when rows_idx is null.  One workgroup per output row; x is read twice, the
-// second time from cache.
+// when rows_idx is null.  One workgroup per output row; x is read once and
+// held in registers for rows up to kThreads * 8 * kNormRegIt columns, longer
+// rows are read twice, the second time from cache.
 template <bool V8>
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restrict__ x,
                                                            uint32_t hidden,
@@ -120,6 +122,45 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float *__restri
     uint16_t *dst = out + static_cast<uint64_t>(i) * hidden;
     float ss = 0.0f;
     if constexpr (V8) {
+        if (hidden <= kThreads * 8 * kNormRegIt) {
+            // The row stays in registers between the two passes, and the
+            // weights load before the reduction; a thread's sum adds the same
+            // terms in the same order as the loop below.  Columns past the
+            // row load its last 8 (not used), so the loads need no branch.
+            floatx4 a[kNormRegIt], b[kNormRegIt];
+            u32x4 wv[kNormRegIt];
+#pragma unroll
+            for (int it = 0; it < kNormRegIt; ++it) {
+                const uint32_t c = min(threadIdx.x * 8 + it * kThreads * 8, hidden - 8);
+                a[it] = *reinterpret_cast<const floatx4 *>(src + c);
+                b[it] = *reinterpret_cast<const floatx4 *>(src + c + 4);
+                wv[it] = *reinterpret_cast<const u32x4 *>(w + c);
+            }
+#pragma unroll
+            for (int it = 0; it < kNormRegIt; ++it) {
+                if (threadIdx.x * 8 + it * kThreads * 8 < hidden) {
+                    ss += a[it][0] * a[it][0] + a[it][1] * a[it][1] + a[it][2] * a[it][2] + a[it][3] * a[it][3];
+                    ss += b[it][0] * b[it][0] + b[it][1] * b[it][1] + b[it][2] * b[it][2] + b[it][3] * b[it][3];
+                }
+            }
+            const float mean_square = block_sum(ss, lds4) / static_cast<float>(hidden);
+            const float inv_rms = 1.0f / sqrtf(mean_square + eps);
+#pragma unroll
+            for (int it = 0; it < kNormRegIt; ++it) {
+                const uint32_t c = threadIdx.x * 8 + it * kThreads * 8;
+                if (c < hidden) {
+                    float wf[8], o[8];
+                    unpack8(wv[it], wf);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        o[k] = wf[k] * (a[it][k] * inv_rms);
+                        o[4 + k] = wf[4 + k] * (b[it][k] * inv_rms);
+                    }
+                    *reinterpret_cast<u32x4 *>(dst + c) = pack8(o);
+                }
+            }
+            return;
+        }
         for (uint32_t c = threadIdx.x * 8; c < hidden; c += kThreads * 8) {
             const floatx4 a = *reinterpret_cast<const floatx4 *>(src + c);
             const floatx4 b = *reinterpret_cast<const floatx4 *>(src + c + 4);
@@ -164,7 +205,15 @@ __global__ __launch_bounds__(kThreads) void add_kernel(float *__restrict__ sum,
 
 __device__ __forceinline__ float silu_mul1(float g, float u) {
     // silu(g) = g * sigmoid(g) = g / (1 + e^-g); times up (cpu/mod.rs:341-349).
-    return g / (1.0f + expf(-g)) * u;
+    // e^-g = 2^(-g log2 e) on the hardware exp2 and the quotient through the
+    // hardware reciprocal (about an ulp each): the f32 value is within ~2^-20
+    // of the correctly rounded one, far inside the bf16 rounding of the
+    // output, and the kernel stays bound by HBM rather than by an exact
+    // exp and divide per element.  Infinities and NaN come out as the exact
+    // form's: g = -inf gives -inf * 0 = NaN, as -inf / inf does.
+    constexpr float kLog2e = 1.44269504088896341f;
+    const float e = __builtin_amdgcn_exp2f(-g * kLog2e);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
 // Backend::silu_mul: out = silu(gate) * up, rows with their own strides;
