@@ -653,7 +653,10 @@ int32_t vo_add(float *sum, const void *x, int32_t x_dtype, uint64_t rows, uint64
  * = gate / (1 + e^-gate) * up, all [rows, cols] bf16 with row strides (in
  * elements) gate_ld, up_ld, out_ld >= cols.  out may be gate itself (the
  * reference's in-place form); gate and up may be the two halves of one
- * fused gate/up projection ([rows, 2*cols], gate_ld = up_ld = 2*cols). */
+ * fused gate/up projection ([rows, 2*cols], gate_ld = up_ld = 2*cols).
+ * e^-gate and the quotient use the GPU's exp2 and reciprocal: the f32 value
+ * is within ~2^-20 of the exact one, each output within one bf16 ulp of the
+ * reference's f32 result. */
 int32_t vo_silu_mul(const void *gate, uint64_t gate_ld, const void *up, uint64_t up_ld,
                     uint64_t rows, uint64_t cols, void *out, uint64_t out_ld, void *stream);
 
