@@ -135,9 +135,11 @@ def test_matmul_rejects_mismatched_shapes(vo, gpu_backend):
     assert e.value.op == "matmul"
 
 
-@pytest.mark.parametrize("t,h", [(5, 19), (33, 4096), (7, 256)])
+@pytest.mark.parametrize("t,h", [(5, 19), (33, 4096), (7, 256), (3, 2056), (2, 8192), (2, 8200)])
 def test_rmsnorm_matches_oracle(vo, gpu_backend, t, h):
-    """cpu/tests.rs:74-96 shape first (the scalar path), then 16-byte rows."""
+    """cpu/tests.rs:74-96 shape first (the scalar path), then 16-byte rows:
+    held in registers up to 8192 columns (2056: one live lane in the second
+    pass of eight columns), read twice beyond (8200)."""
     import torch
     _say(f"rmsnorm {t}x{h}")
     x = orc.rand_vec(5, t * h).reshape(t, h) * np.float32(3.0)
